@@ -1,0 +1,154 @@
+"""Benchmark of the exact Lloyd pass on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload outliers_d32]
+
+A step is one Lloyd iteration over the whole workload (assignment, compensated per-cluster accumulation,
+float64 centre update and stopping test), run by the engine's GPU-resident loop with the data already in HBM.
+The default workload is 10M x 32 float32, k=64, with 1% outliers (synthetic, seeded). The JSON line carries the
+per-pass time, the dominant kernel's achieved HBM bandwidth measured with HIP events on the engine's stream,
+and the CPU baseline (this repository's restatement of the reference's multithreaded C++ pass, kmeans.mm,
+timed on the host's cores over a row sample and scaled to the full workload).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "mlx-kmeans_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "ms per Lloyd pass + achieved % of HBM/MFMA roofline, 10M×32 fp32 k=64"
+HBM_PEAK_GBS = 8000.0          # MI355X published HBM3E bandwidth
+FP32_PEAK_TFLOPS = 157.3       # MI355X published fp32 (matrix) peak
+BF16_PEAK_TFLOPS = 2500.0      # MI355X published dense bf16 MFMA peak
+
+DESCRIPTIONS = {
+    "outliers_d32": "10M x 32 fp32, k=64, 64-component mixture + 1% uniform outliers, k-means++ start",
+    "blobs_d32": "100k x 32 fp32, k=64, 64-component mixture, k-means++ start",
+    "lowd_d8": "10M x 8 fp32, k=8, 8-component diagonal mixture",
+    "pixels_d4": "96M x 4 fp32, k=12, 12-class clipped correlated mixture",
+    "embed_d768": "1M x 768 fp32, k=1024, unit-norm vMF-style embeddings",
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def profile_summary(name):
+    """HBM traffic per launch from a committed rocprofv3 --pmc summary, if one exists for this workload."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def cpu_baseline(X, C, budget_s=12.0):
+    import oracle
+    cores = max(1, min(16, os.cpu_count() or 1))
+    n = len(X)
+    rows = min(n, 2_000_000)
+    sample = X[:rows]
+    oracle.cpu_pass(sample[: min(rows, 50_000)], C, nthreads=cores)    # warm
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle.cpu_pass(sample, C, nthreads=cores)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > budget_s or len(times) >= 20:
+            break
+    per_pass_ms = float(np.median(times)) * 1e3 * (n / rows)
+    return {"value": round(per_pass_ms, 3), "unit": "ms/pass", "cores": cores, "kind": "port",
+            "sample": f"first {rows:,} of {n:,} rows, {len(times)} passes, median scaled by {n / rows:g}; "
+                      f"kmeans.mm CPU backend restated (oracle/kmeans_oracle.c orc_cpu_pass)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="outliers_d32", choices=sorted(DESCRIPTIONS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported (the Lloyd pass shards by rows; "
+              f"the multi-GPU exchange is design-only in this build)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mlx_kmeans import _lib, synthetic
+
+    log(f"[bench] generating {a.workload}")
+    w = synthetic.WORKLOADS[a.workload]()
+    X, C0, k = w["X"], w["C0"], w["k"]
+    n, d = X.shape
+    ctx = _lib.Context(0)
+    ctx.set_parts([X])
+    log(f"[bench] data on device: {n} x {d}, k={k}")
+
+    # warmup, then exactly `steps` Lloyd iterations timed by the host clock around device synchronisations
+    ctx.fit(C0, a.warmup, 0.0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    C, inertia, iters, _ = ctx.fit(C0, a.steps, 0.0)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert iters == a.steps, (iters, a.steps)
+    ms = elapsed * 1e3 / a.steps
+    log(f"[bench] {a.steps} passes in {elapsed * 1e3:.3f} ms -> {ms:.4f} ms/pass, path {ctx.last_path()}")
+
+    # dominant kernel: HIP events around every launch on the engine's stream, over the same loop
+    ctx.profile(True)
+    ctx.fit(C0, a.steps, 0.0)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kname, (kms, kcount) = max(prof.items(), key=lambda kv: kv[1][0])
+    avg_ms = kms / kcount
+    log("[bench] kernels: " + ", ".join(f"{k_}: {v[0] / v[1] * 1e3:.1f} us x{v[1]}" for k_, v in prof.items()))
+    if a.workload == "embed_d768":
+        flops = 2.0 * n * k * d
+        achieved = flops / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": profile_summary(a.workload),
+                "kernel": kname, "kernel_avg_ms": round(avg_ms, 5)}
+    else:
+        bytes_alg = float(n) * d * 4
+        achieved = bytes_alg / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_summary(a.workload),
+                "kernel": kname, "kernel_avg_ms": round(avg_ms, 5), "bytes_per_launch": bytes_alg}
+    cpu = None if a.no_cpu else cpu_baseline(X, C0)
+    out = {
+        "metric": METRIC,
+        "value": round(ms, 5),
+        "unit": "ms/pass",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{a.workload}: {DESCRIPTIONS[a.workload]}", "rows": n, "dims": d, "k": k,
+                   "parallelism": "single GPU"},
+        "rows_per_s": round(n / (ms * 1e-3)),
+        "final_inertia": inertia,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+/*
+ * kmeans_hip.h - C ABI of libkmeans_hip.so, the MI355X (gfx950) engine for the exact Lloyd pass.
+ *
+ * Plain pointers and sizes only. Every entry point returns KM_OK (0) or a negative code; the message for the
+ * last failure on a context is km_last_error(ctx). Each context owns one HIP stream (default priority), its
+ * device copies of the data and its workspaces; calls on one context must not overlap (one context per host
+ * thread). Citations name the reference (kakollu/mlx-kmeans) interface each entry point replaces.
+ *
+ * Data layout: rows are float32, row-major (rows, dims), C-contiguous - the reference's layout
+ * (mlx_kmeans/estimator.py:120). Centres are float32 (k, dims). Totals are float64 (k, dims + 2) in the
+ * reference's column order [count, sum of best distance, sum of x_0 .. x_{dims-1}] (core.py:1629-1636).
+ *
+ * Exactness contract (mode KM_EXACT): every label is the centre with the smallest float32 distance
+ * s = sum_j (x_j - c_j)^2, accumulated for j ascending with the product and the add rounded separately,
+ * lowest index on an exact tie (the rows loop, core.py:263-274); best is that s. Whatever kernel path runs,
+ * the labels and best values are these, bit for bit.
+ */
+#ifndef KMEANS_HIP_H
+#define KMEANS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct km_ctx km_ctx;
+
+/* return codes */
+#define KM_OK 0
+#define KM_EINVAL (-1)      /* bad argument: the message carries the reference's wording where one exists */
+#define KM_EDEVICE (-2)     /* a HIP call or a kernel launch failed */
+#define KM_ENOMEM (-3)      /* device allocation failed */
+#define KM_ENODATA (-4)     /* no data set on the context */
+
+/* where a pointer argument lives */
+#define KM_HOST 0
+#define KM_DEVICE 1
+
+/* assignment mode: exact=True / exact=False of the reference's KMeans (estimator.py:67-69) */
+#define KM_EXACT 0
+#define KM_APPROX 1
+
+/* kernel path, the reference's `method` argument (core.py:2018): AUTO picks by shape */
+#define KM_PATH_AUTO 0
+#define KM_PATH_ROWS 1      /* direct-form scan of every centre on the vector ALUs (the reference's "rows") */
+#define KM_PATH_MFMA 2      /* bf16 matrix-core screen + exact rescoring of the candidates (the reference's "tiles") */
+
+/* Create a context on HIP device `device` (ordinal). NULL on failure (no context to carry a message).
+ * Replaces the reference's module-global per-dataset caches (core.py:548-578): all state lives here. */
+km_ctx *km_create(int32_t device);
+
+/* Free every device buffer and the stream. NULL is accepted. */
+void km_destroy(km_ctx *ctx);
+
+/* Message for the last failure on ctx ("" if none). Valid until the next call on ctx. */
+const char *km_last_error(const km_ctx *ctx);
+
+/* Set the data to one slice of `rows` x `dims` float32. where = KM_HOST copies it to the device (the
+ * context owns the copy); where = KM_DEVICE borrows a device pointer, which must stay valid and unchanged
+ * until the data is replaced or the context destroyed. Replaces KMeans._parts (estimator.py:108-125). */
+int32_t km_set_data(km_ctx *ctx, const float *X, int64_t rows, int32_t dims, int32_t where);
+
+/* Append one more slice with the same dims (the reference's list-of-slices input, estimator.py:110-111).
+ * Totals are summed over slices; labels come back concatenated in slice order. */
+int32_t km_append_data(km_ctx *ctx, const float *X, int64_t rows, int32_t where);
+
+/* Total rows over all slices, and dims (0 if no data). */
+int64_t km_rows(const km_ctx *ctx);
+int32_t km_dims(const km_ctx *ctx);
+
+/* One assignment pass with centres C (host, k x dims) and no update.
+ *   totals: host (k, dims+2) float64, required.
+ *   labels: host uint32 per row, or NULL.   best: host float32 per row, or NULL.
+ * Replaces _gpu_pass (core.py:2018-2197), which assign_mlx (core.py:2200-2206) wraps. */
+int32_t km_pass(km_ctx *ctx, const float *C, int32_t k, int32_t mode, int32_t path, double *totals,
+                uint32_t *labels, float *best);
+
+/* One Lloyd iteration from centres C (host, k x dims): C_out (host, k x dims) gets the new centres,
+ * *inertia the inertia of C (before the update), *n_empty the number of clusters that came up empty and
+ * were relocated as scikit-learn does. Replaces lloyd_step (core.py:2209-2242). */
+int32_t km_lloyd_step(km_ctx *ctx, const float *C, int32_t k, int32_t mode, int32_t path, float *C_out,
+                      double *inertia, int32_t *n_empty);
+
+/* Up to max_iter Lloyd iterations from C0 (host, k x dims) with the reference's stopping rule
+ * |prev - inertia| <= tol * prev (estimator.py:147-149), spherical renormalisation when spherical != 0
+ * (estimator.py:127-130, 141-142). Iterations run back to back on the device; the host looks at the
+ * device-side state only every few iterations and when a cluster empties. Outputs (host): C_out the final
+ * centres, *last_inertia the inertia reported by the last iteration, *n_iter the iterations run,
+ * *n_relocated the total empty clusters relocated. Replaces KMeans._one_run's loop (estimator.py:132-150). */
+int32_t km_fit(km_ctx *ctx, const float *C0, int32_t k, int32_t max_iter, double tol, int32_t mode,
+               int32_t spherical, float *C_out, double *last_inertia, int32_t *n_iter, int32_t *n_relocated);
+
+/* Kernel timing with HIP events on the context's stream. km_profile(ctx, 1) clears and starts recording;
+ * km_profile_read gives, for kernel id `kernel`, the summed milliseconds and launch count so far.
+ * km_kernel_name(id) names an id ("" past the last); ids are stable within one build. */
+int32_t km_profile(km_ctx *ctx, int32_t enable);
+int32_t km_profile_read(km_ctx *ctx, int32_t kernel, double *ms_total, int64_t *launches);
+const char *km_kernel_name(int32_t kernel);
+
+/* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS or KM_PATH_MFMA), and the number of
+ * rows the MFMA screen could not settle alone (rescored against every centre) in that pass. */
+int32_t km_last_path(const km_ctx *ctx);
+int64_t km_last_fallback_rows(km_ctx *ctx);
+
+/* ABI version of this header. */
+int32_t km_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

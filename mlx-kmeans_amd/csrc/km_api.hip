@@ -1,0 +1,635 @@
+// libkmeans_hip.so: the C ABI (include/kmeans_hip.h) and the host runtime around the kernels.
+//
+// A context owns one HIP stream, the device copies (or borrowed pointers) of the data slices, the current
+// centres, and every workspace of a pass. A Lloyd iteration is a fixed sequence of kernels on that stream:
+//   prep (centre norms, bf16 operand)  ->  assignment + accumulation into per-block partials
+//   ->  reduce to float64 totals  ->  update stats (counts, inertia, empties, stopping rule)
+//   ->  update centres (in place)  [-> spherical renormalisation]
+// The update kernels keep the loop state in a device-side km_control block, and every kernel of a pass is
+// gated on it, so km_fit queues iterations back to back and looks at the state only every KM_FIT_BATCH
+// iterations. A pass that leaves clusters empty stops the queue; the host then relocates them the way the
+// reference's lloyd_step does (core.py:2222-2242) and resumes.
+#include "kmeans_hip.h"
+#include "km_internal.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#define KM_ABI_VERSION 1
+static const int KM_FIT_BATCH = 8;
+
+template <class T>
+struct DBuf {
+    T *p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t n) {
+        if (n <= cap && p) return hipSuccess;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        if (n == 0) n = 1;
+        hipError_t e = hipMalloc((void **)&p, n * sizeof(T));
+        if (e == hipSuccess) cap = n;
+        else p = nullptr;
+        return e;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+struct Part {
+    const float *X;   // device pointer used by kernels
+    float *owned;     // non-null when the context allocated X
+    int64_t rows;
+    bool aligned;     // 16-byte aligned: whole-float4 row loads are allowed
+};
+
+struct ProfRec {
+    int kernel;
+    hipEvent_t a, b;
+};
+
+struct km_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<Part> parts;
+    int32_t d = 0;
+    int64_t n = 0;
+    std::string err;
+    int32_t last_path = 0;
+    DBuf<float> C;          // current centres (k, d)
+    DBuf<float> csq, cnorm, maxes;
+    DBuf<uint16_t> cb;
+    DBuf<float> psum, pcomp;
+    DBuf<double> tot;
+    DBuf<double> tot2;      // (k, 2) [count, best] totals recomputed for km_pass on the fused path
+    DBuf<uint32_t> labels;
+    DBuf<float> best;
+    km_control *ctl = nullptr;    // device
+    km_control *ctl_h = nullptr;  // pinned host mirror
+    bool prof = false;
+    std::vector<ProfRec> recs;
+    std::vector<hipEvent_t> pool;
+    double prof_ms[KK_COUNT] = {};
+    int64_t prof_n[KK_COUNT] = {};
+};
+
+static int fail(km_ctx *c, int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf;
+    return code;
+}
+
+#define HIPCHK(ctx, expr)                                                                                 \
+    do {                                                                                                  \
+        hipError_t e_ = (expr);                                                                           \
+        if (e_ != hipSuccess)                                                                             \
+            return fail((ctx), e_ == hipErrorOutOfMemory ? KM_ENOMEM : KM_EDEVICE, "%s failed: %s (%s:%d)", \
+                        #expr, hipGetErrorString(e_), __FILE__, __LINE__);                                \
+    } while (0)
+
+static hipEvent_t get_event(km_ctx *c) {
+    if (!c->pool.empty()) {
+        hipEvent_t e = c->pool.back();
+        c->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Launch through f, bracketed by events on the context's stream when timing is on.
+template <class F>
+static hipError_t launch(km_ctx *c, int kid, F &&f) {
+    if (!c->prof) return f();
+    hipEvent_t a = get_event(c), b = get_event(c);
+    if (!a || !b) return f();
+    (void)hipEventRecord(a, c->stream);
+    hipError_t e = f();
+    (void)hipEventRecord(b, c->stream);
+    c->recs.push_back({kid, a, b});
+    return e;
+}
+
+static void harvest(km_ctx *c) {
+    if (c->recs.empty()) return;
+    (void)hipStreamSynchronize(c->stream);
+    for (auto &r : c->recs) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+            c->prof_ms[r.kernel] += ms;
+            c->prof_n[r.kernel] += 1;
+        }
+        c->pool.push_back(r.a);
+        c->pool.push_back(r.b);
+    }
+    c->recs.clear();
+}
+
+// ------------------------------------------------------------------ context and data
+
+extern "C" km_ctx *km_create(int32_t device) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return nullptr;
+    if (hipSetDevice(device) != hipSuccess) return nullptr;
+    km_ctx *c = new km_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return nullptr;
+    }
+    if (hipMalloc((void **)&c->ctl, sizeof(km_control)) != hipSuccess ||
+        hipHostMalloc((void **)&c->ctl_h, sizeof(km_control), hipHostMallocDefault) != hipSuccess) {
+        if (c->ctl) (void)hipFree(c->ctl);
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return nullptr;
+    }
+    memset(c->ctl_h, 0, sizeof(km_control));
+    return c;
+}
+
+static void drop_parts(km_ctx *c) {
+    for (auto &p : c->parts)
+        if (p.owned) (void)hipFree(p.owned);
+    c->parts.clear();
+    c->n = 0;
+    c->d = 0;
+}
+
+extern "C" void km_destroy(km_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    drop_parts(c);
+    c->C.release();
+    c->csq.release();
+    c->cnorm.release();
+    c->maxes.release();
+    c->cb.release();
+    c->psum.release();
+    c->pcomp.release();
+    c->tot.release();
+    c->tot2.release();
+    c->labels.release();
+    c->best.release();
+    for (auto &r : c->recs) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    for (auto e : c->pool) (void)hipEventDestroy(e);
+    if (c->ctl) (void)hipFree(c->ctl);
+    if (c->ctl_h) (void)hipHostFree(c->ctl_h);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+extern "C" const char *km_last_error(const km_ctx *c) { return c ? c->err.c_str() : "no context"; }
+
+static int add_part(km_ctx *c, const float *X, int64_t rows, int32_t where) {
+    if (!X) return fail(c, KM_EINVAL, "data pointer is null");
+    if (rows < 1) return fail(c, KM_EINVAL, "expected a nonempty 2-D (rows, dims) array, got %lld rows", (long long)rows);
+    Part p{nullptr, nullptr, rows, true};
+    if (where == KM_DEVICE) {
+        p.X = X;
+        p.aligned = ((uintptr_t)X % 16) == 0;
+    } else if (where == KM_HOST) {
+        const size_t bytes = (size_t)rows * c->d * sizeof(float);
+        HIPCHK(c, hipMalloc((void **)&p.owned, bytes));
+        hipError_t e = hipMemcpyAsync(p.owned, X, bytes, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(p.owned);
+            return fail(c, KM_EDEVICE, "copying the data to the device failed: %s", hipGetErrorString(e));
+        }
+        p.X = p.owned;
+    } else {
+        return fail(c, KM_EINVAL, "where must be KM_HOST or KM_DEVICE");
+    }
+    c->parts.push_back(p);
+    c->n += rows;
+    return KM_OK;
+}
+
+extern "C" int32_t km_set_data(km_ctx *c, const float *X, int64_t rows, int32_t dims, int32_t where) {
+    if (!c) return KM_EINVAL;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    drop_parts(c);
+    if (dims < 1) return fail(c, KM_EINVAL, "expected a nonempty 2-D (rows, dims) array, got %d dims", dims);
+    c->d = dims;
+    int r = add_part(c, X, rows, where);
+    if (r != KM_OK) c->d = 0;
+    return r;
+}
+
+extern "C" int32_t km_append_data(km_ctx *c, const float *X, int64_t rows, int32_t where) {
+    if (!c) return KM_EINVAL;
+    if (c->parts.empty()) return fail(c, KM_ENODATA, "no data: call km_set_data first");
+    HIPCHK(c, hipSetDevice(c->device));
+    return add_part(c, X, rows, where);
+}
+
+extern "C" int64_t km_rows(const km_ctx *c) { return c ? c->n : 0; }
+extern "C" int32_t km_dims(const km_ctx *c) { return c ? c->d : 0; }
+extern "C" int32_t km_version(void) { return KM_ABI_VERSION; }
+extern "C" int32_t km_last_path(const km_ctx *c) { return c ? c->last_path : 0; }
+
+extern "C" int64_t km_last_fallback_rows(km_ctx *c) {
+    if (!c) return -1;
+    if (hipMemcpyAsync(c->ctl_h, c->ctl, sizeof(km_control), hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        return -1;
+    return (int64_t)c->ctl_h->fallback_rows;
+}
+
+// ------------------------------------------------------------------ one pass
+
+static int check_centres(km_ctx *c, const float *C, int32_t k) {
+    if (c->parts.empty()) return fail(c, KM_ENODATA, "no data: call km_set_data first");
+    if (!C) return fail(c, KM_EINVAL, "centres pointer is null");
+    if (k < 1) return fail(c, KM_EINVAL, "n_clusters must be a positive integer");
+    return KM_OK;
+}
+
+// Decide the assignment path for this shape. MFMA when the screen serves the shape and pays; rows otherwise.
+static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
+    *mp = km_plan_mfma(c->n, c->d, k, 1);
+    for (auto &p : c->parts)
+        if (!p.aligned) mp->ok = 0;
+    if (path == KM_PATH_ROWS) return KM_PATH_ROWS;
+    if (path == KM_PATH_MFMA) return mp->ok ? KM_PATH_MFMA : -1;
+    // auto: the screen pays once a row's distance work is large enough to hide its epilogue
+    if (mp->ok && c->d >= 16 && (int64_t)k * c->d >= 256) return KM_PATH_MFMA;
+    return KM_PATH_ROWS;
+}
+
+// Sizes the per-pass workspaces. Returns KM_OK or an error.
+static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bool need_rows_scratch) {
+    const int64_t kw = (int64_t)k * (c->d + 2);
+    HIPCHK(c, c->psum.ensure(total_rb * (size_t)kw));
+    HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)kw));
+    HIPCHK(c, c->tot.ensure((size_t)kw));
+    if (need_rows_scratch) {
+        HIPCHK(c, c->labels.ensure((size_t)c->n));
+        HIPCHK(c, c->best.ensure((size_t)c->n));
+    }
+    (void)chosen;
+    return KM_OK;
+}
+
+static km_centre_aux aux_of(km_ctx *c) {
+    km_centre_aux a;
+    a.csq = c->csq.p;
+    a.cnorm = c->cnorm.p;
+    a.maxes = c->maxes.p;
+    a.cb = c->cb.p;
+    return a;
+}
+
+// One assignment + accumulation pass over every slice with the centres in c->C, leaving float64 totals in
+// c->tot. labels_d/best_d: device arrays of n (or null) to receive the per-row results. gated: every kernel
+// checks ctl->stop.
+static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, float *best_d, bool gated) {
+    (void)mode;
+    km_mfma_plan mp;
+    const int chosen = choose_path(c, k, path, &mp);
+    if (chosen < 0)
+        return fail(c, KM_EINVAL, "path=mfma does not serve k=%d, dims=%d on this build", k, c->d);
+    c->last_path = chosen;
+    const int32_t *stop = gated ? &c->ctl->stop : nullptr;
+    const int d = c->d;
+    const int64_t kw = (int64_t)k * (d + 2);
+
+    if (chosen == KM_PATH_MFMA) {
+        size_t total_rb = 0;
+        std::vector<km_mfma_plan> plans;
+        for (auto &p : c->parts) {
+            plans.push_back(km_plan_mfma(p.rows, d, k, 1));
+            total_rb += plans.back().nrb;
+        }
+        int r = ensure_pass_buffers(c, k, chosen, total_rb, false);
+        if (r) return r;
+        HIPCHK(c, c->csq.ensure(mp.kpad));
+        HIPCHK(c, c->cnorm.ensure(mp.kpad));
+        HIPCHK(c, c->maxes.ensure(4));
+        HIPCHK(c, c->cb.ensure((size_t)mp.kpad * mp.dpad));
+        km_centre_aux aux = aux_of(c);
+        HIPCHK(c, launch(c, KK_PREP, [&] { return km_launch_prep(c->C.p, k, d, mp.kpad, mp.dpad, aux, stop, c->stream); }));
+        int rb = 0;
+        int64_t row0 = 0;
+        for (size_t i = 0; i < c->parts.size(); i++) {
+            const Part &p = c->parts[i];
+            uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
+            float *bst = best_d ? best_d + row0 : nullptr;
+            HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
+                return km_launch_mfma(plans[i], 1, p.X, p.rows, d, c->C.p, k, aux, lab, bst, c->psum.p, c->pcomp.p,
+                                      rb, c->ctl, stop, c->stream);
+            }));
+            rb += plans[i].nrb;
+            row0 += p.rows;
+        }
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->tot.p, stop, c->stream); }));
+        return KM_OK;
+    }
+
+    // rows path: exact labels for every slice, then the generic accumulation
+    size_t total_rb = 0;
+    std::vector<km_accum_plan> plans;
+    for (auto &p : c->parts) {
+        plans.push_back(km_plan_accum_generic(p.rows, d, k));
+        total_rb += plans.back().nrb;
+    }
+    int r = ensure_pass_buffers(c, k, chosen, total_rb, true);
+    if (r) return r;
+    uint32_t *lab_all = labels_d ? labels_d : c->labels.p;
+    float *best_all = best_d ? best_d : c->best.p;
+    int rb = 0;
+    int64_t row0 = 0;
+    for (size_t i = 0; i < c->parts.size(); i++) {
+        const Part &p = c->parts[i];
+        HIPCHK(c, launch(c, KK_ASSIGN_ROWS, [&] {
+            return km_launch_assign_rows(p.X, p.rows, d, c->C.p, k, lab_all + row0, best_all + row0, stop, c->stream);
+        }));
+        HIPCHK(c, launch(c, KK_ACCUM_GENERIC, [&] {
+            return km_launch_accum_generic(plans[i], p.X, p.rows, d, lab_all + row0, best_all + row0, k, c->psum.p,
+                                           c->pcomp.p, rb, stop, c->stream);
+        }));
+        rb += plans[i].nrb;
+        row0 += p.rows;
+    }
+    HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->tot.p, stop, c->stream); }));
+    return KM_OK;
+}
+
+// Labels and best for every row with the centres in c->C, into c->labels / c->best (no accumulation needed by
+// the caller, but the pass runs in full: it is the same code as every other pass, so the same bits).
+static int run_labels(km_ctx *c, int k, int mode, int path) {
+    HIPCHK(c, c->labels.ensure((size_t)c->n));
+    HIPCHK(c, c->best.ensure((size_t)c->n));
+    return run_pass(c, k, mode, path, c->labels.p, c->best.p, false);
+}
+
+static int upload_centres(km_ctx *c, const float *C, int k) {
+    HIPCHK(c, c->C.ensure((size_t)k * c->d));
+    HIPCHK(c, hipMemcpyAsync(c->C.p, C, (size_t)k * c->d * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    return KM_OK;
+}
+
+static int reset_control(km_ctx *c, double tol) {
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    memset(c->ctl_h, 0, sizeof(km_control));
+    c->ctl_h->tol = tol;
+    HIPCHK(c, hipMemcpyAsync(c->ctl, c->ctl_h, sizeof(km_control), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KM_OK;
+}
+
+static int read_control(km_ctx *c) {
+    HIPCHK(c, hipMemcpyAsync(c->ctl_h, c->ctl, sizeof(km_control), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KM_OK;
+}
+
+static int write_control(km_ctx *c) {
+    HIPCHK(c, hipMemcpyAsync(c->ctl, c->ctl_h, sizeof(km_control), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KM_OK;
+}
+
+extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, int32_t path, double *totals,
+                           uint32_t *labels, float *best) {
+    if (!c) return KM_EINVAL;
+    int r = check_centres(c, C, k);
+    if (r) return r;
+    if (!totals) return fail(c, KM_EINVAL, "totals pointer is null");
+    HIPCHK(c, hipSetDevice(c->device));
+    if ((r = upload_centres(c, C, k))) return r;
+    HIPCHK(c, c->labels.ensure((size_t)c->n));
+    HIPCHK(c, c->best.ensure((size_t)c->n));
+    if ((r = reset_control(c, 0.0))) return r;
+    if ((r = run_pass(c, k, mode, path, c->labels.p, c->best.p, false))) return r;
+    const int w = c->d + 2;
+    const int64_t kw = (int64_t)k * w;
+    HIPCHK(c, hipMemcpyAsync(totals, c->tot.p, kw * sizeof(double), hipMemcpyDeviceToHost, c->stream));
+    std::vector<double> cb2;
+    if (c->last_path == KM_PATH_MFMA) {
+        // The fused screen keeps the per-cluster sums of x but only the pass total of best (column 1 of
+        // cluster 0). The per-cluster best sums come from one more deterministic accumulation over the
+        // [count, best] columns alone, reading the labels and best this pass wrote.
+        std::vector<km_accum_plan> plans;
+        size_t total_rb = 0;
+        for (auto &p : c->parts) {
+            plans.push_back(km_plan_accum_generic(p.rows, 0, k));
+            total_rb += plans.back().nrb;
+        }
+        HIPCHK(c, c->psum.ensure(total_rb * (size_t)k * 2));
+        HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)k * 2));
+        HIPCHK(c, c->tot2.ensure((size_t)k * 2));
+        int rb = 0;
+        int64_t row0 = 0;
+        for (size_t i = 0; i < c->parts.size(); i++) {
+            const Part &p = c->parts[i];
+            HIPCHK(c, launch(c, KK_ACCUM_GENERIC, [&] {
+                return km_launch_accum_generic(plans[i], nullptr, p.rows, 0, c->labels.p + row0, c->best.p + row0, k,
+                                               c->psum.p, c->pcomp.p, rb, nullptr, c->stream);
+            }));
+            rb += plans[i].nrb;
+            row0 += p.rows;
+        }
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, c->tot2.p, nullptr, c->stream); }));
+        cb2.resize((size_t)k * 2);
+        HIPCHK(c, hipMemcpyAsync(cb2.data(), c->tot2.p, cb2.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
+    }
+    if (labels) HIPCHK(c, hipMemcpyAsync(labels, c->labels.p, c->n * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+    if (best) HIPCHK(c, hipMemcpyAsync(best, c->best.p, c->n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (!cb2.empty())
+        for (int j = 0; j < k; j++) totals[(size_t)j * w + 1] = cb2[(size_t)j * 2 + 1];
+    harvest(c);
+    return KM_OK;
+}
+
+// ------------------------------------------------------------------ relocation of empty clusters (host side)
+//
+// The pass whose stats kernel flagged empties left its totals in c->tot and its input centres in c->C.
+// Following lloyd_step (core.py:2222-2242): the empty clusters, in ascending order, take the rows with the
+// largest best distance (ties: lower row index); each such row leaves its old cluster; centres are the
+// float64 means rounded to float32; a cluster still empty takes the largest cluster's centre.
+static int relocate(km_ctx *c, int k, int mode, int path, int *n_empty_out) {
+    const int d = c->d, w = d + 2;
+    std::vector<double> tot((size_t)k * w);
+    HIPCHK(c, hipMemcpyAsync(tot.data(), c->tot.p, tot.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    std::vector<int64_t> counts(k);
+    std::vector<double> sums((size_t)k * d);
+    std::vector<int> empty;
+    for (int j = 0; j < k; j++) {
+        counts[j] = llrint(tot[(size_t)j * w]);
+        for (int e = 0; e < d; e++) sums[(size_t)j * d + e] = tot[(size_t)j * w + 2 + e];
+        if (counts[j] == 0) empty.push_back(j);
+    }
+    *n_empty_out = (int)empty.size();
+    if (!empty.empty()) {
+        int r = run_labels(c, k, mode, path);
+        if (r) return r;
+        std::vector<float> best(c->n);
+        std::vector<uint32_t> labels(c->n);
+        HIPCHK(c, hipMemcpyAsync(best.data(), c->best.p, c->n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(labels.data(), c->labels.p, c->n * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        float bmax = 0.0f;
+        for (float b : best) bmax = std::max(bmax, b);
+        if (bmax > 0.0f) {
+            const int64_t m = std::min<int64_t>((int64_t)empty.size(), c->n);
+            std::vector<int64_t> idx(c->n);
+            for (int64_t i = 0; i < c->n; i++) idx[i] = i;
+            auto farther = [&](int64_t a, int64_t b) { return best[a] > best[b] || (best[a] == best[b] && a < b); };
+            std::partial_sort(idx.begin(), idx.begin() + m, idx.end(), farther);
+            std::vector<float> row(d);
+            for (int64_t t = 0; t < m; t++) {
+                const int64_t f = idx[t];
+                // locate row f in its slice
+                int64_t off = f;
+                const float *src = nullptr;
+                for (auto &p : c->parts) {
+                    if (off < p.rows) { src = p.X + off * d; break; }
+                    off -= p.rows;
+                }
+                HIPCHK(c, hipMemcpy(row.data(), src, d * sizeof(float), hipMemcpyDeviceToHost));
+                const int nw = empty[t], old = (int)labels[f];
+                for (int e = 0; e < d; e++) sums[(size_t)old * d + e] -= (double)row[e];
+                counts[old] -= 1;
+                for (int e = 0; e < d; e++) sums[(size_t)nw * d + e] = (double)row[e];
+                counts[nw] = 1;
+            }
+        }
+    }
+    std::vector<float> Cn((size_t)k * d);
+    int big = 0;
+    for (int j = 1; j < k; j++)
+        if (counts[j] > counts[big]) big = j;
+    for (int j = 0; j < k; j++)
+        if (counts[j] > 0)
+            for (int e = 0; e < d; e++) Cn[(size_t)j * d + e] = (float)(sums[(size_t)j * d + e] / (double)counts[j]);
+    for (int j = 0; j < k; j++)
+        if (counts[j] <= 0)
+            for (int e = 0; e < d; e++) Cn[(size_t)j * d + e] = Cn[(size_t)big * d + e];
+    HIPCHK(c, hipMemcpyAsync(c->C.p, Cn.data(), Cn.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KM_OK;
+}
+
+// Queues pass `pass` of a loop: the pass itself, then the update stage.
+static int queue_iteration(km_ctx *c, int k, int mode, int path, int pass, double tol, int spherical) {
+    int r = run_pass(c, k, mode, path, nullptr, nullptr, true);
+    if (r) return r;
+    const int d = c->d;
+    HIPCHK(c, launch(c, KK_UPDATE_STATS, [&] { return km_launch_update_stats(c->tot.p, k, d + 2, c->ctl, pass, tol, c->stream); }));
+    HIPCHK(c, launch(c, KK_UPDATE_CENTRES, [&] { return km_launch_update_centres(c->tot.p, k, d, c->ctl, pass, c->C.p, c->stream); }));
+    if (spherical)
+        HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->C.p, k, d, c->ctl, pass, c->stream); }));
+    return KM_OK;
+}
+
+extern "C" int32_t km_lloyd_step(km_ctx *c, const float *C, int32_t k, int32_t mode, int32_t path, float *C_out,
+                                 double *inertia, int32_t *n_empty) {
+    if (!c) return KM_EINVAL;
+    int r = check_centres(c, C, k);
+    if (r) return r;
+    if (!C_out) return fail(c, KM_EINVAL, "C_out pointer is null");
+    HIPCHK(c, hipSetDevice(c->device));
+    if ((r = upload_centres(c, C, k))) return r;
+    if ((r = reset_control(c, 0.0))) return r;
+    if ((r = queue_iteration(c, k, mode, path, 0, 0.0, 0))) return r;
+    if ((r = read_control(c))) return r;
+    int ne = c->ctl_h->n_empty;
+    if (c->ctl_h->need_reloc) {
+        if ((r = relocate(c, k, mode, path, &ne))) return r;
+    }
+    HIPCHK(c, hipMemcpyAsync(C_out, c->C.p, (size_t)k * c->d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (inertia) *inertia = c->ctl_h->inertia;
+    if (n_empty) *n_empty = ne;
+    harvest(c);
+    return KM_OK;
+}
+
+extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_iter, double tol, int32_t mode,
+                          int32_t spherical, float *C_out, double *last_inertia, int32_t *n_iter,
+                          int32_t *n_relocated) {
+    if (!c) return KM_EINVAL;
+    int r = check_centres(c, C0, k);
+    if (r) return r;
+    if (max_iter < 1) return fail(c, KM_EINVAL, "max_iter must be a positive integer");
+    if (!(tol >= 0.0) || !std::isfinite(tol)) return fail(c, KM_EINVAL, "tol must be finite and nonnegative");
+    HIPCHK(c, hipSetDevice(c->device));
+    if ((r = upload_centres(c, C0, k))) return r;
+    if ((r = reset_control(c, tol))) return r;
+    if (spherical) HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->C.p, k, c->d, c->ctl, -1, c->stream); }));
+    const int path = KM_PATH_AUTO;
+    int pass = 0, relocated = 0;
+    while (pass < max_iter) {
+        const int batch = std::min(KM_FIT_BATCH, max_iter - pass);
+        for (int i = 0; i < batch; i++)
+            if ((r = queue_iteration(c, k, mode, path, pass + i, tol, spherical))) return r;
+        if ((r = read_control(c))) return r;
+        pass = c->ctl_h->iter;
+        if (c->ctl_h->need_reloc) {
+            int ne = 0;
+            if ((r = relocate(c, k, mode, path, &ne))) return r;
+            relocated += ne;
+            if (spherical) HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->C.p, k, c->d, c->ctl, -1, c->stream); }));
+            c->ctl_h->need_reloc = 0;
+            c->ctl_h->stop = c->ctl_h->done;
+            if ((r = write_control(c))) return r;
+        }
+        if (c->ctl_h->done) break;
+    }
+    if (C_out) HIPCHK(c, hipMemcpyAsync(C_out, c->C.p, (size_t)k * c->d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (last_inertia) *last_inertia = c->ctl_h->inertia;
+    if (n_iter) *n_iter = c->ctl_h->iter;
+    if (n_relocated) *n_relocated = relocated;
+    harvest(c);
+    return KM_OK;
+}
+
+// ------------------------------------------------------------------ timing
+
+extern "C" int32_t km_profile(km_ctx *c, int32_t enable) {
+    if (!c) return KM_EINVAL;
+    harvest(c);
+    for (int i = 0; i < KK_COUNT; i++) {
+        c->prof_ms[i] = 0.0;
+        c->prof_n[i] = 0;
+    }
+    c->prof = enable != 0;
+    return KM_OK;
+}
+
+extern "C" int32_t km_profile_read(km_ctx *c, int32_t kernel, double *ms_total, int64_t *launches) {
+    if (!c) return KM_EINVAL;
+    if (kernel < 0 || kernel >= KK_COUNT) return fail(c, KM_EINVAL, "kernel id %d out of range", kernel);
+    harvest(c);
+    if (ms_total) *ms_total = c->prof_ms[kernel];
+    if (launches) *launches = c->prof_n[kernel];
+    return KM_OK;
+}
+
+extern "C" const char *km_kernel_name(int32_t kernel) {
+    return (kernel >= 0 && kernel < KK_COUNT) ? km_kernel_names[kernel] : "";
+}

@@ -1,0 +1,338 @@
+// Generic kernels of the exact Lloyd pass: they serve every (rows, dims, k) and define the semantics that the
+// faster paths reproduce bit for bit.
+//
+//   k_assign_rows     exact nearest centre, one row per lane, direct form over every centre
+//                     (reference: mlx_kmeans/core.py:263-274, the rows loop)
+//   k_accum_generic   deterministic compensated per-cluster [count, best, x] into per-row-block partials
+//                     (reference: the accumulation paths of core.py:1292-1466; Neumaier add of core.py:244-247)
+//   k_reduce          partials -> float64 totals in row-block order
+//   k_update_stats    counts, inertia, empties, argmax, stopping rule (core.py:2222-2242, estimator.py:147-149)
+//   k_update_centres  centres = sums / counts in float64, rounded to float32 (core.py:2238-2242)
+//   k_normalise       spherical renormalisation (estimator.py:127-130)
+//
+// The file is compiled with -ffp-contract=off: `s + t * t` stays a separately rounded product and add.
+#pragma clang fp contract(off)
+#include "km_internal.h"
+#include <math.h>
+
+const char *const km_kernel_names[KK_COUNT] = {
+    "km_prep", "km_assign_rows", "km_accum_generic", "km_reduce", "km_update_stats",
+    "km_update_centres", "km_normalise", "km_fused_rows", "km_fused_mfma", "km_assign_mfma"};
+
+// Neumaier's compensated add, the reference's KAHAN_ADD (core.py:244-247): t = s + v; the rounding error of
+// that add goes to c; the true running sum is s + c.
+__device__ __forceinline__ void neumaier(float &s, float &c, float v) {
+    float t = s + v;
+    c += (fabsf(s) >= fabsf(v)) ? ((s - t) + v) : ((v - t) + s);
+    s = t;
+}
+
+// ------------------------------------------------------------------ exact assignment, one row per lane
+
+template <int D>
+__global__ __launch_bounds__(256) void k_assign_rows(const float *__restrict__ X, int64_t n, int d_rt,
+                                                     const float *__restrict__ C, int k,
+                                                     uint32_t *__restrict__ labels, float *__restrict__ best,
+                                                     const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float bst = INFINITY;
+    uint32_t bl = 0;
+    if constexpr (D > 0) {
+        const float *x = X + i * D;
+        float xv[D];
+#pragma unroll
+        for (int j = 0; j < D; j++) xv[j] = x[j];
+        for (int c = 0; c < k; c++) {
+            const float *cc = C + (size_t)c * D;
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < D; j++) {
+                float t = xv[j] - cc[j];
+                s = s + t * t;
+            }
+            if (s < bst) { bst = s; bl = (uint32_t)c; }
+        }
+    } else {
+        const int d = d_rt;
+        const float *x = X + i * d;
+        for (int c = 0; c < k; c++) {
+            const float *cc = C + (size_t)c * d;
+            float s = 0.0f;
+            for (int j = 0; j < d; j++) {
+                float t = x[j] - cc[j];
+                s = s + t * t;
+            }
+            if (s < bst) { bst = s; bl = (uint32_t)c; }
+        }
+    }
+    if (labels) labels[i] = bl;
+    if (best) best[i] = bst;
+}
+
+hipError_t km_launch_assign_rows(const float *X, int64_t n, int d, const float *C, int k, uint32_t *labels,
+                                 float *best, const int32_t *stop, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    dim3 grid((unsigned)((n + 255) / 256)), block(256);
+#define KM_ROWS_CASE(DD) \
+    case DD: hipLaunchKernelGGL(k_assign_rows<DD>, grid, block, 0, s, X, n, d, C, k, labels, best, stop); break;
+    switch (d) {
+        KM_ROWS_CASE(1) KM_ROWS_CASE(2) KM_ROWS_CASE(3) KM_ROWS_CASE(4) KM_ROWS_CASE(5) KM_ROWS_CASE(6)
+        KM_ROWS_CASE(7) KM_ROWS_CASE(8) KM_ROWS_CASE(10) KM_ROWS_CASE(12) KM_ROWS_CASE(16) KM_ROWS_CASE(24)
+        KM_ROWS_CASE(32) KM_ROWS_CASE(48) KM_ROWS_CASE(64)
+        default: hipLaunchKernelGGL(k_assign_rows<0>, grid, block, 0, s, X, n, d, C, k, labels, best, stop);
+    }
+#undef KM_ROWS_CASE
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ generic deterministic accumulation
+//
+// Grid: x = row-block, y = cluster-block, z = column-block; 256 threads. Columns of a cluster are
+// [count, best, x_0, ..., x_{d-1}] (w = d + 2). The block scans its rows in ascending order, 256 at a time,
+// and keeps the rows whose label falls in its cluster range, in ascending order. Those rows are dealt to P
+// "slots" in turn (entry q of a chunk to slot q % P); a slot is DL threads, one column each, and has its own
+// LDS accumulator copy, so every accumulator has exactly one writer and a fixed order of adds. At the end
+// the copies are folded in slot order and written as this row-block's partial: a sum and a compensation.
+// The result depends only on the data and the plan, never on scheduling.
+
+static int next_pow2(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+static constexpr size_t KM_ACC_LDS_BUDGET = 48 * 1024;
+
+km_accum_plan km_plan_accum_generic(int64_t n, int d, int k) {
+    km_accum_plan pl{};
+    const int w = d + 2;
+    pl.wb = w < 2048 ? w : 2048;
+    pl.nwb = (w + pl.wb - 1) / pl.wb;
+    const int dl = next_pow2(pl.wb < 256 ? pl.wb : 256);
+    const int P = 256 / dl;
+    int cb = (int)(KM_ACC_LDS_BUDGET / 8 / ((size_t)P * pl.wb));
+    if (cb < 1) cb = 1;
+    if (cb > k) cb = k;
+    pl.cb = cb;
+    pl.ncb = (k + cb - 1) / cb;
+    // enough blocks to fill the chip several times over, but row-blocks of at least 2048 rows
+    int64_t target_rb = (2048 + (int64_t)pl.ncb * pl.nwb - 1) / ((int64_t)pl.ncb * pl.nwb);
+    if (target_rb < 1) target_rb = 1;
+    int64_t rbs = (n + target_rb - 1) / target_rb;
+    if (rbs < 2048) rbs = 2048;
+    rbs = (rbs + 255) / 256 * 256;
+    pl.rbs = rbs;
+    pl.nrb = (int)((n + rbs - 1) / rbs);
+    if (pl.nrb < 1) pl.nrb = 1;
+    pl.lds = (size_t)P * cb * pl.wb * 2 * sizeof(float) + (256 + 8) * sizeof(int);
+    return pl;
+}
+
+__global__ __launch_bounds__(256) void k_accum_generic(const float *__restrict__ X, int64_t n, int d,
+                                                       const uint32_t *__restrict__ labels,
+                                                       const float *__restrict__ best, int k, int CB, int WB,
+                                                       int DL, int64_t RBS, float *__restrict__ psum,
+                                                       float *__restrict__ pcomp, int rb0,
+                                                       const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ float lds[];
+    const int w = d + 2;
+    const int P = 256 / DL;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c0 = blockIdx.y * CB;
+    const int cb = min(CB, k - c0);
+    const int e_lo = blockIdx.z * WB;
+    const int ww = min(WB, w - e_lo);
+    float *acc = lds;
+    float *cmp = lds + (size_t)P * CB * WB;
+    int *list = (int *)(cmp + (size_t)P * CB * WB);
+    int *wcount = list + 256;
+    for (int e = tid; e < P * CB * WB; e += 256) { acc[e] = 0.0f; cmp[e] = 0.0f; }
+    const int64_t r_begin = (int64_t)blockIdx.x * RBS;
+    const int64_t r_end = min(n, r_begin + RBS);
+    const int slot = tid / DL, le = tid % DL;
+    __syncthreads();
+    for (int64_t r0 = r_begin; r0 < r_end; r0 += 256) {
+        const int64_t r = r0 + tid;
+        bool m = false;
+        if (r < r_end) {
+            const uint32_t L = labels[r];
+            m = (L >= (uint32_t)c0) && (L < (uint32_t)(c0 + cb));
+        }
+        const uint64_t bal = __ballot(m);
+        const int before = __popcll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) wcount[wave] = __popcll(bal);
+        __syncthreads();
+        int off = 0;
+        for (int v = 0; v < wave; v++) off += wcount[v];
+        const int M = wcount[0] + wcount[1] + wcount[2] + wcount[3];
+        if (m) list[off + before] = tid;
+        __syncthreads();
+        for (int q = slot; q < M; q += P) {
+            const int64_t row = r0 + list[q];
+            const int L = (int)labels[row] - c0;
+            float *a = acc + ((size_t)slot * CB + L) * WB;
+            float *cc = cmp + ((size_t)slot * CB + L) * WB;
+            for (int e = le; e < ww; e += DL) {
+                const int col = e_lo + e;
+                const float v = col >= 2 ? X[row * d + (col - 2)] : (col == 0 ? 1.0f : best[row]);
+                neumaier(a[e], cc[e], v);
+            }
+        }
+        __syncthreads();
+    }
+    const int64_t kw = (int64_t)k * w;
+    for (int e = tid; e < cb * ww; e += 256) {
+        const int cl = e / ww, col = e % ww;
+        const size_t o = (size_t)cl * WB + col;
+        float s = acc[o], c = cmp[o];
+        for (int p = 1; p < P; p++) {
+            neumaier(s, c, acc[(size_t)p * CB * WB + o]);
+            c += cmp[(size_t)p * CB * WB + o];
+        }
+        const int64_t dst = (int64_t)(rb0 + blockIdx.x) * kw + (int64_t)(c0 + cl) * w + e_lo + col;
+        psum[dst] = s;
+        pcomp[dst] = c;
+    }
+}
+
+hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int64_t n, int d,
+                                   const uint32_t *labels, const float *best, int k, float *psum,
+                                   float *pcomp, int rb0, const int32_t *stop, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int dl = next_pow2(pl.wb < 256 ? pl.wb : 256);
+    dim3 grid(pl.nrb, pl.ncb, pl.nwb), block(256);
+    hipLaunchKernelGGL(k_accum_generic, grid, block, pl.lds, s, X, n, d, labels, best, k, pl.cb, pl.wb, dl,
+                       pl.rbs, psum, pcomp, rb0, stop);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ partials -> float64 totals
+
+__global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ psum, const float *__restrict__ pcomp,
+                                                int nrb, int64_t kw, double *__restrict__ tot,
+                                                const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= kw) return;
+    double s = 0.0;
+    for (int r = 0; r < nrb; r++) s += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
+    tot[e] = s;
+}
+
+hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tot,
+                            const int32_t *stop, hipStream_t s) {
+    dim3 grid((unsigned)((kw + 255) / 256)), block(256);
+    hipLaunchKernelGGL(k_reduce, grid, block, 0, s, psum, pcomp, nrb, kw, tot, stop);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ update stage
+
+// One block of 256 threads. Counts are rint(tot[c, 0]) (exact integers in every partial). The inertia is the
+// sum of tot[:, 1] in a fixed order (per-thread strided sums, then a fixed tree), so it is reproducible.
+__global__ __launch_bounds__(256) void k_update_stats(const double *__restrict__ tot, int k, int w,
+                                                      km_control *__restrict__ ctl, int pass, double tol) {
+    if (ctl->stop) return;
+    __shared__ double s_in[256];
+    __shared__ int s_empty[256];
+    __shared__ long long s_max[256];
+    __shared__ int s_arg[256];
+    const int tid = threadIdx.x;
+    double in = 0.0;
+    int empty = 0;
+    long long mx = -1;
+    int arg = 0;
+    for (int c = tid; c < k; c += 256) {
+        const long long cnt = llrint(tot[(size_t)c * w]);
+        in += tot[(size_t)c * w + 1];
+        empty += cnt == 0;
+        if (cnt > mx) { mx = cnt; arg = c; }   // strided ascending c: first maximum within this thread
+    }
+    s_in[tid] = in;
+    s_empty[tid] = empty;
+    s_max[tid] = mx;
+    s_arg[tid] = arg;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if (tid < h) {
+            s_in[tid] += s_in[tid + h];
+            s_empty[tid] += s_empty[tid + h];
+            const long long mo = s_max[tid + h];
+            const int ao = s_arg[tid + h];
+            if (mo > s_max[tid] || (mo == s_max[tid] && ao < s_arg[tid])) { s_max[tid] = mo; s_arg[tid] = ao; }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const double inertia = s_in[0];
+        const int ne = s_empty[0];
+        int done = 0;
+        if (pass > 0 && fabs(ctl->prev - inertia) <= tol * ctl->prev) done = 1;
+        ctl->prev = inertia;
+        ctl->inertia = inertia;
+        ctl->n_empty = ne;
+        ctl->big = s_arg[0];
+        ctl->need_reloc = (ne > 0 && inertia > 0.0) ? 1 : 0;
+        ctl->done = done;
+        ctl->iter = pass + 1;
+        ctl->stop = (done || ctl->need_reloc) ? 1 : 0;
+    }
+}
+
+hipError_t km_launch_update_stats(const double *tot, int k, int w, km_control *ctl, int pass, double tol,
+                                  hipStream_t s) {
+    hipLaunchKernelGGL(k_update_stats, dim3(1), dim3(256), 0, s, tot, k, w, ctl, pass, tol);
+    return hipGetLastError();
+}
+
+// C[c, j] = float(sum / count). Runs only for the pass whose stats just completed (ctl->iter == pass + 1)
+// and only when no relocation is pending (the host performs that update). A cluster still empty here can
+// only be one with no rows to give it (every best was 0): it takes the largest cluster's centre.
+__global__ __launch_bounds__(256) void k_update_centres(const double *__restrict__ tot, int k, int d,
+                                                        const km_control *__restrict__ ctl, int pass,
+                                                        float *__restrict__ C) {
+    if (ctl->iter != pass + 1 || ctl->need_reloc) return;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (int64_t)k * d) return;
+    const int w = d + 2;
+    int c = (int)(e / d);
+    const int j = (int)(e % d);
+    long long cnt = llrint(tot[(size_t)c * w]);
+    if (cnt <= 0) {
+        c = ctl->big;
+        cnt = llrint(tot[(size_t)c * w]);
+    }
+    C[e] = (float)(tot[(size_t)c * w + 2 + j] / (double)cnt);
+}
+
+hipError_t km_launch_update_centres(const double *tot, int k, int d, km_control *ctl, int pass, float *C,
+                                    hipStream_t s) {
+    const int64_t kd = (int64_t)k * d;
+    hipLaunchKernelGGL(k_update_centres, dim3((unsigned)((kd + 255) / 256)), dim3(256), 0, s, tot, k, d, ctl,
+                       pass, C);
+    return hipGetLastError();
+}
+
+// Spherical k-means: each centre divided by its length (float32 division by the float32-rounded norm, which is
+// summed in float64), a zero centre left as is. pass < 0 runs unconditionally (the start of a fit).
+__global__ __launch_bounds__(64) void k_normalise(float *__restrict__ C, int k, int d,
+                                                  const km_control *__restrict__ ctl, int pass) {
+    if (pass >= 0 && (ctl->iter != pass + 1 || ctl->need_reloc)) return;
+    const int c = blockIdx.x;
+    if (c >= k) return;
+    float *row = C + (size_t)c * d;
+    double s = 0.0;
+    for (int j = threadIdx.x; j < d; j += 64) s += (double)row[j] * (double)row[j];
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    const float nrm = (float)sqrt(s);
+    if (nrm > 0.0f)
+        for (int j = threadIdx.x; j < d; j += 64) row[j] = row[j] / nrm;
+}
+
+hipError_t km_launch_normalise(float *C, int k, int d, const km_control *ctl, int pass, hipStream_t s) {
+    hipLaunchKernelGGL(k_normalise, dim3(k), dim3(64), 0, s, C, k, d, ctl, pass);
+    return hipGetLastError();
+}

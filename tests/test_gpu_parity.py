@@ -1,0 +1,213 @@
+"""GPU parity: the HIP engine against the CPU oracle, through the C ABI.
+
+Labels and best distances must be bit-identical to the oracle's (the reference's exact mode, core.py:263-274)
+on every kernel path; counts exact; sums within 1e-6 of the data's RMS per centre and inertia within 1e-6
+relative (tests/accuracy.py:91-99); new centres within 1e-6 of the RMS (the same criterion) after each Lloyd
+step. At full size, where the oracle cannot run every row, labels are checked on a random sample of rows and
+the totals through identities that hold at any size.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+import make_golden as G  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+CENTRE_TOL = 1e-6      # |centre - reference| / RMS(X)   (tests/accuracy.py:91-97)
+INERTIA_TOL = 1e-6     # relative                      (tests/accuracy.py:98)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mlx_kmeans import _lib
+    _lib.lib()
+    return _lib
+
+
+def mfma_served(d, k):
+    return d in (16, 32) and k <= 128 or d == 64 and k <= 32
+
+
+def check_totals(tot, X, labels, best, ref_tot, scale):
+    k = tot.shape[0]
+    counts = np.rint(tot[:, 0]).astype(np.int64)
+    ref_counts = np.rint(ref_tot[:, 0]).astype(np.int64)
+    assert np.array_equal(counts, ref_counts)
+    used = ref_counts > 0
+    err = np.max(np.abs(tot[used, 2:] - ref_tot[used, 2:]) / ref_counts[used, None]) / scale if used.any() else 0.0
+    assert err <= CENTRE_TOL, err
+    ri = float(ref_tot[:, 1].sum())
+    assert abs(float(tot[:, 1].sum()) - ri) <= INERTIA_TOL * max(ri, 1e-30)
+    assert k == ref_tot.shape[0]
+
+
+@pytest.mark.parametrize("path", ["rows", "mfma"])
+@pytest.mark.parametrize("name", G.CASES)
+def test_pass_matches_oracle(lib, name, path):
+    fx = np.load(G.fixture_path(name))
+    parts, C0, steps = G.case_inputs(name)
+    d, k = C0.shape[1], C0.shape[0]
+    if path == "mfma" and not mfma_served(d, k):
+        pytest.skip(f"mfma path serves d in (16, 32) with k <= 128 and d=64 with k <= 32, not d={d} k={k}")
+    X = np.concatenate(parts)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean())) or 1.0
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    C = fx["C0"]
+    for s in range(steps):
+        say(f"[gpu] pass {name} step {s} path={path} n={len(X)} d={d} k={k}")
+        tot, labels, best = ctx.run_pass(C, path=lib.PATHS[path], labels=True, best=True)
+        assert ctx.last_path() == path
+        assert np.array_equal(labels, fx[f"labels_{s}"].astype(np.uint32)), f"labels differ at step {s}"
+        assert np.array_equal(best.view(np.uint32), fx[f"best_{s}"].view(np.uint32)), f"best differs at step {s}"
+        check_totals(tot, X, labels, best, fx[f"tot_{s}"], scale)
+        # per-cluster best sums are exact on every path
+        np.testing.assert_allclose(tot[:, 1], fx[f"tot_{s}"][:, 1], rtol=1e-6, atol=1e-30)
+        C = fx[f"centres_{s + 1}"]
+    ctx.close()
+
+
+@pytest.mark.parametrize("name", G.CASES)
+def test_lloyd_step_matches_oracle(lib, name):
+    fx = np.load(G.fixture_path(name))
+    parts, C0, steps = G.case_inputs(name)
+    X = np.concatenate(parts)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean())) or 1.0
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    C = fx["C0"]
+    for s in range(steps):
+        say(f"[gpu] lloyd_step {name} step {s}")
+        C_new, inertia, n_empty = ctx.lloyd_step(C)
+        assert n_empty == int(fx[f"n_empty_{s}"])
+        ri = float(fx[f"inertia_{s}"])
+        assert abs(inertia - ri) <= INERTIA_TOL * max(ri, 1e-30)
+        ref = fx[f"centres_{s + 1}"]
+        err = float(np.max(np.abs(C_new.astype(np.float64) - ref.astype(np.float64)))) / scale
+        assert err <= CENTRE_TOL, (s, err)
+        C = ref            # continue from the oracle's centres so a float32 tie cannot compound
+    ctx.close()
+
+
+@pytest.mark.parametrize("name", ["blobs_d32", "outliers_d32", "lowd_d8", "relocation_d16_k32", "slices_d16_k100"])
+def test_fit_loop_matches_oracle(lib, name):
+    import oracle
+    fx = np.load(G.fixture_path(name))
+    parts, C0, steps = G.case_inputs(name)
+    X = np.concatenate(parts)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    say(f"[gpu] fit {name} iters={steps}")
+    C, last_inertia, n_iter, n_rel = ctx.fit(fx["C0"], steps, 0.0)
+    assert n_iter == steps
+    assert n_rel == sum(int(fx[f"n_empty_{s}"]) for s in range(steps))
+    ref = fx[f"centres_{steps}"]
+    assert float(np.max(np.abs(C.astype(np.float64) - ref))) / scale <= 10 * CENTRE_TOL
+    ri = float(fx[f"inertia_{steps - 1}"])
+    assert abs(last_inertia - ri) <= 1e-5 * ri
+    # the stopping rule: with a loose tol the loop stops early, and C is the centres after the stopping step
+    ref_C, _, ref_iter, _ = oracle.fit_from(X, fx["C0"], max_iter=50, tol=1e-2)
+    C2, _, it2, _ = ctx.fit(fx["C0"], 50, 1e-2)
+    assert it2 == ref_iter
+    assert float(np.max(np.abs(C2.astype(np.float64) - ref_C))) / scale <= 10 * CENTRE_TOL
+    ctx.close()
+
+
+def test_paths_are_bit_identical(lib):
+    rng = np.random.default_rng(5)
+    for d, k in [(32, 64), (16, 128), (32, 128), (64, 32), (16, 32)]:
+        X = (rng.uniform(-3, 3, size=(k // 4, d))[rng.integers(0, k // 4, 60_000)]
+             + rng.standard_normal((60_000, d))).astype(np.float32)
+        C = X[rng.choice(len(X), k, replace=False)]
+        ctx = lib.Context()
+        ctx.set_parts([X])
+        say(f"[gpu] paths d={d} k={k}")
+        t1, l1, b1 = ctx.run_pass(C, path=lib.KM_PATH_ROWS, labels=True, best=True)
+        t2, l2, b2 = ctx.run_pass(C, path=lib.KM_PATH_MFMA, labels=True, best=True)
+        assert np.array_equal(l1, l2) and np.array_equal(b1.view(np.uint32), b2.view(np.uint32))
+        assert np.array_equal(np.rint(t1[:, 0]), np.rint(t2[:, 0]))
+        ctx.close()
+
+
+def test_reruns_are_bit_identical(lib):
+    parts, C0, _ = G.case_inputs("outliers_d32")
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    say("[gpu] reruns")
+    a = ctx.run_pass(C0, labels=True, best=True)
+    b = ctx.run_pass(C0, labels=True, best=True)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+    f1 = ctx.fit(C0, 5, 0.0)
+    f2 = ctx.fit(C0, 5, 0.0)
+    assert np.array_equal(f1[0], f2[0]) and f1[1] == f2[1]
+    ctx.close()
+
+
+def test_estimator_known_answer_and_restarts():
+    # tests/test_files.py:67-79
+    from unittest.mock import patch
+    from mlx_kmeans import KMeans
+    X = np.array([[0., 0.], [1., 0.], [9., 0.], [10., 0.]], np.float32)
+    say("[gpu] estimator known answer")
+    fitted = KMeans(n_clusters=2, max_iter=1, random_state=3).fit(X)
+    expected = np.min(((X[:, None] - fitted.cluster_centers_) ** 2).sum(2), axis=1).sum()
+    assert abs(fitted.inertia_ - float(expected)) < 1e-5
+    good = np.array([[.5, 0], [9.5, 0]], np.float32)
+    bad = np.array([[0, 0], [1, 0]], np.float32)
+    with patch.object(KMeans, '_one_run', side_effect=[(bad, 0., 1), (good, 999., 1)]):
+        fitted = KMeans(n_clusters=2, n_init=2).fit(X)
+    np.testing.assert_equal(fitted.cluster_centers_, good)
+    assert abs(fitted.inertia_ - 1.0) < 1e-7
+    assert fitted.labels_.dtype == np.int64 and fitted.labels_.tolist() == [0, 0, 1, 1]
+    with pytest.raises(ValueError, match="features"):
+        fitted.predict(np.zeros((3, 5), np.float32))
+
+
+def test_estimator_nonfinite_is_explained():
+    from mlx_kmeans import KMeans
+    X = np.random.default_rng(0).standard_normal((1000, 4)).astype(np.float32)
+    X[10, 2] = np.nan
+    say("[gpu] estimator nan")
+    with pytest.raises(ValueError, match="NaN or infinity"):
+        KMeans(n_clusters=4, max_iter=3, random_state=0).fit(X)
+
+
+def test_headline_workload_full_size(lib):
+    """10M x 32, k=64 with 1% outliers: labels of a 200k-row sample bit-identical to the oracle's; counts sum to
+    n; the per-cluster sums add up to the column sums of X; a rerun gives the same bits."""
+    import oracle
+    from mlx_kmeans import synthetic
+    w = synthetic.outliers_d32()
+    X, C0 = w["X"], w["C0"]
+    n = len(X)
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] headline full size n={n}")
+    tot, labels, best = ctx.run_pass(C0, labels=True, best=True)
+    assert ctx.last_path() == "mfma"
+    rng = np.random.default_rng(1)
+    idx = np.sort(rng.choice(n, 200_000, replace=False))
+    ol, ob = oracle.assign(X[idx], C0)
+    assert np.array_equal(labels[idx], ol)
+    assert np.array_equal(best[idx].view(np.uint32), ob.view(np.uint32))
+    assert int(np.rint(tot[:, 0]).sum()) == n
+    colsum = X.astype(np.float64).sum(0)
+    assert np.max(np.abs(tot[:, 2:].sum(0) - colsum)) <= 1e-6 * np.abs(X).sum(0).max()
+    tot2, labels2, _ = ctx.run_pass(C0, labels=True)
+    assert np.array_equal(tot, tot2) and np.array_equal(labels, labels2)
+    # the fit loop's first iteration equals a pass + the oracle's update on the same labels
+    C1, inertia, n_empty = ctx.lloyd_step(C0)
+    C1_ref, inertia_ref, _ = oracle.update(oracle.totals(X, labels, best, 64), X, labels, best, C0)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    assert float(np.max(np.abs(C1.astype(np.float64) - C1_ref))) / scale <= CENTRE_TOL
+    assert abs(inertia - inertia_ref) <= INERTIA_TOL * inertia_ref
+    ctx.close()
