@@ -359,16 +359,16 @@ __global__ __launch_bounds__(64 * KM_WAVES) void k_fused_mfma(
             const uint32_t L1 = __builtin_amdgcn_readlane(lab_mine, 2 * i + 1);
             if (L0 == 0xffffffffu) break;   // rows past the end come last in a tile
             const uint32_t L = half ? L1 : L0;
-            const bool act = (half == 0 || L1 != 0xffffffffu) && j < D;
+            const bool act = (half == 0 || L1 != 0xffffffffu) && j < D;   // D < 32: lanes past D idle
 #define KM_KAHAN_UPD()                                              \
-    {                                                               \
-        const float xv = TT[(2 * i + half) * D + j];                \
-        float2 sc = acc[L * D + j];                                 \
+    for (int jj = j; jj < D; jj += 32) {                            \
+        const float xv = TT[(2 * i + half) * D + jj];               \
+        float2 sc = acc[L * D + jj];                                \
         const float y = xv - sc.y;                                  \
         const float tt = sc.x + y;                                  \
         sc.y = (tt - sc.x) - y;                                     \
         sc.x = tt;                                                  \
-        acc[L * D + j] = sc;                                        \
+        acc[L * D + jj] = sc;                                       \
     }
             if (L0 != L1) {
                 if (act) KM_KAHAN_UPD();
@@ -466,8 +466,8 @@ struct fused_entry {
 
 static fused_entry g_fused[] = {
     KM_FUSED(16, 32), KM_FUSED(16, 64), KM_FUSED(16, 128),
-    KM_FUSED(32, 32), KM_FUSED(32, 64), KM_FUSED(32, 128),
-    KM_FUSED(64, 32), KM_FUSED(64, 64),
+    KM_FUSED(32, 32), KM_FUSED(32, 64),
+    KM_FUSED(64, 32),
 };
 #undef KM_FUSED
 
