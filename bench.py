@@ -77,7 +77,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="outliers_d32", choices=sorted(DESCRIPTIONS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 1 GiB with torch (a plain copy kernel of known size, for counter calibration)")
     a = ap.parse_args()
+    if a.copy_probe:
+        import torch
+        x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": x.numel() * 4}), flush=True)
+        return
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported (the Lloyd pass shards by rows; "
               f"the multi-GPU exchange is design-only in this build)", file=sys.stderr)

@@ -326,7 +326,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         HIPCHK(c, c->csq.ensure(mp.kpad));
         HIPCHK(c, c->cnorm.ensure(mp.kpad));
         HIPCHK(c, c->maxes.ensure(4));
-        HIPCHK(c, c->cb.ensure((size_t)mp.kpad * mp.dpad));
+        HIPCHK(c, c->cb.ensure((size_t)mp.kpad * (mp.dpad + 16)));
         km_centre_aux aux = aux_of(c);
         HIPCHK(c, launch(c, KK_PREP, [&] { return km_launch_prep(c->C.p, k, d, mp.kpad, mp.dpad, aux, stop, c->stream); }));
         int rb = 0;

@@ -82,6 +82,7 @@ struct km_mfma_plan {
     int kpad, dpad;  // padded centre count and dims
     int64_t rbs;     // rows per block (fused)
     int nrb;         // blocks
+    int waves;       // waves per block
     size_t lds;
 };
 km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused);

@@ -31,38 +31,54 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ centre preparation
 
-// csq (float32 of the float64 sum), cnorm (|c| rounded up), padding centres get csq = FLT_MAX (never a
-// candidate, and finite so packed keys stay ordered numbers), and the bf16(-2c) operand in MFMA A order:
-// cb[((t * DS + s) * 64 + lane) * 8 + q] = bf16(-2 * C[32t + (lane & 31), (lane >> 5) * DH + 8s + q]).
+// csq (float32 of the float64 sum), cnorm (|c| rounded up), padding centres get csq = 3e38 (never a
+// candidate, and finite so packed keys stay ordered numbers), and the MFMA A operand. For centre tile t and
+// K-step s < DS: cb[((t * (DS+1) + s) * 64 + lane) * 8 + q] = bf16(-2 * C[32t + (lane & 31), (lane >> 5) * DH + 8s + q]).
+// K-step DS carries |c|^2 as two bf16 pieces (q = 0, 1 of the half-0 lanes) against a B operand of ones, so the
+// screen value |c|^2 - 2 x.c comes out of the matrix cores with no accumulator initialisation.
 __global__ __launch_bounds__(256) void k_prep(const float *__restrict__ C, int k, int d, int kpad, int dpad,
                                               float *__restrict__ csq, float *__restrict__ cnorm,
                                               uint16_t *__restrict__ cb, const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int DS = dpad / 16, DH = dpad / 2;
-    const int64_t total = (int64_t)kpad * dpad;
+    const int64_t total = (int64_t)kpad * (dpad + 16);
     if (e < total) {
         const int q = (int)(e & 7);
         const int lane = (int)((e >> 3) & 63);
         const int64_t ts = e >> 9;
-        const int s = (int)(ts % DS), t = (int)(ts / DS);
+        const int s = (int)(ts % (DS + 1)), t = (int)(ts / (DS + 1));
         const int c = 32 * t + (lane & 31);
-        const int j = (lane >> 5) * DH + 8 * s + q;
         float v = 0.0f;
-        if (c < k && j < d) v = -2.0f * C[(size_t)c * d + j];
+        if (s < DS) {
+            const int j = (lane >> 5) * DH + 8 * s + q;
+            if (c < k && j < d) v = -2.0f * C[(size_t)c * d + j];
+        } else if ((lane >> 5) == 0 && q < 2) {
+            double sq = 3.0e38;
+            if (c < k) {
+                sq = 0.0;
+                for (int j = 0; j < d; j++) {
+                    const double x = C[(size_t)c * d + j];
+                    sq += x * x;
+                }
+            }
+            const float sf = (float)sq;
+            const float hi = (float)(__bf16)sf;
+            v = (q == 0) ? hi : (sf - hi);
+        }
         __bf16 b = (__bf16)v;
         cb[e] = *reinterpret_cast<uint16_t *>(&b);
     }
     if (e < kpad) {
         const int c = (int)e;
         if (c < k) {
-            double s = 0.0;
+            double sq = 0.0;
             for (int j = 0; j < d; j++) {
-                const double v = C[(size_t)c * d + j];
-                s += v * v;
+                const double x = C[(size_t)c * d + j];
+                sq += x * x;
             }
-            csq[c] = (float)s;
-            cnorm[c] = (float)(sqrt(s) * (1.0 + 1e-6));
+            csq[c] = (float)sq;
+            cnorm[c] = (float)(sqrt(sq) * (1.0 + 1e-6));
         } else {
             csq[c] = 3.0e38f;
             cnorm[c] = 0.0f;
@@ -99,7 +115,7 @@ __global__ __launch_bounds__(256) void k_prep_max(const float *__restrict__ csq,
 
 hipError_t km_launch_prep(const float *C, int k, int d, int kpad, int dpad, km_centre_aux aux,
                           const int32_t *stop, hipStream_t s) {
-    const int64_t total = (int64_t)kpad * dpad;
+    const int64_t total = (int64_t)kpad * (dpad + 16);
     const int64_t m = total > kpad ? total : kpad;
     hipLaunchKernelGGL(k_prep, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, C, k, d, kpad, dpad, aux.csq,
                        aux.cnorm, aux.cb, stop);
@@ -110,290 +126,493 @@ hipError_t km_launch_prep(const float *C, int k, int d, int kpad, int dpad, km_c
 }
 
 // ------------------------------------------------------------------ the fused kernel
+//
+// Exactness of the screen. For a row x and centre c let A_c = |c|^2 - 2 x.c (exact reals) and D_c = |x - c|^2 =
+// |x|^2 + A_c. The matrix cores give a'_c; with bf16 rounding of x and c (relative 2^-9 each), the float32
+// accumulation of DP + 2 products (gamma_{DP+2}), the two-piece |c|^2 (2^-17) and bf16 denormal flushing,
+//     |a'_c - A_c| <= E = BETA |x| max|c| + GAM2 max|c|^2 + FLUSH (|x| + max|c|) + TINY      (uniform in c).
+// The float32 direct form s_c of the rows loop satisfies |s_c - D_c| <= g D_c + eta, g = gamma_{D+2}. A centre c
+// can hold the row's minimum only if s_c <= s_m for the screen's minimiser m, which forces
+//     a'_c - a'_m <= 2E + 2 g/(1-g) D_m + tiny,   D_m <= |x|^2 + a'_m + E,
+// so every centre outside T = a'_m + that margin is ruled out, and rescoring the ones inside in ascending index
+// with a strict '<' returns exactly the rows loop's label and best. The screen keys carry a local index in
+// their low IB mantissa bits (a relative perturbation of at most RHO), which the test absorbs.
 
-__device__ __forceinline__ float shfl32(float v) { return __shfl_xor(v, 32); }
-__device__ __forceinline__ uint32_t shfl32u(uint32_t v) { return (uint32_t)__shfl_xor((int)v, 32); }
+__device__ __forceinline__ uint32_t u32(float v) { return __float_as_uint(v); }
+__device__ __forceinline__ float f32(uint32_t v) { return __uint_as_float(v); }
+
+// v_permlane32_swap: lane l < 32 gets (va of lane l, va of lane l+32); lane l >= 32 gets (vb of lane l-32,
+// vb of lane l). With va the tile-A value and vb the tile-B value of this lane's half row, every lane receives
+// (half 0, half 1) of the row it owns: tile A row l for l < 32, tile B row l-32 for l >= 32.
+__device__ __forceinline__ void own_halves(float va, float vb, float &h0, float &h1) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u32(va), u32(vb), false, false);
+    h0 = f32(r[0]);
+    h1 = f32(r[1]);
+}
+__device__ __forceinline__ void own_halves_u(uint32_t va, uint32_t vb, uint32_t &h0, uint32_t &h1) {
+    const auto r = __builtin_amdgcn_permlane32_swap(va, vb, false, false);
+    h0 = r[0];
+    h1 = r[1];
+}
+// value of lane l ^ 32
+__device__ __forceinline__ float partner(float v, int lane) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u32(v), u32(v), false, false);
+    return f32(lane < 32 ? r[1] : r[0]);
+}
 
 // Error-window constants. u = 2^-24 (float32 unit roundoff); gamma_m = m u / (1 - m u).
 __host__ __device__ constexpr double km_gamma(int m) { return m * 5.9604644775390625e-08 / (1.0 - m * 5.9604644775390625e-08); }
 
-template <int D, int KP, bool ACCUM>
-__global__ __launch_bounds__(64 * KM_WAVES) void k_fused_mfma(
-    const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k, const float *__restrict__ csq,
-    const float *__restrict__ maxes, const uint16_t *__restrict__ cbg, int64_t rbs, uint32_t *__restrict__ labels,
-    float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp, int rb0,
-    km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
-    constexpr int DP = (D + 15) / 16 * 16;   // padded dims
-    constexpr int DH = DP / 2;               // dims per lane half
-    constexpr int DS = DP / 16;              // MFMA K-steps
-    constexpr int KT = KP / 32;              // centre tiles
-    constexpr int NV = KT * 16;              // screen values per lane
-    constexpr int IB = NV <= 16 ? 4 : NV <= 32 ? 5 : NV <= 64 ? 6 : 7;   // index bits packed into keys
-    constexpr int CS = D + 4;                // LDS row stride of the float32 centres
-    constexpr int W = D + 2;
-    // window constants (see the derivation in the header of this file and in the design notes)
-    constexpr float BETA = (float)(2.0 * (0x1p-8 + 0x1p-18) * (1.0 + 0x1p-20) + 2.01 * km_gamma(DP + 1));
-    constexpr float GAM2 = (float)(km_gamma(DP + 1) + 0x1p-24);
+template <int D, int KP>
+struct Geo {
+    static constexpr int DP = (D + 15) / 16 * 16;   // padded dims
+    static constexpr int DH = DP / 2;               // dims per lane half
+    static constexpr int DS = DP / 16;              // MFMA K-steps over the dims (one more carries |c|^2)
+    static constexpr int KT = KP / 32;              // centre tiles
+    static constexpr int IB = KT <= 1 ? 4 : KT <= 2 ? 5 : 6;   // index bits packed into keys (16 KT values)
+    static constexpr int CS = D + 4;                // LDS row stride of the float32 centres
+    static constexpr int AS = D + 1;                // LDS row stride of the accumulators
+};
+
+// Screen one 32-row tile: x is this lane's half row. Returns the smallest and second smallest packed key over
+// this lane's 16 KT screen values.
+template <int D, int KP>
+__device__ __forceinline__ void screen_tile(const float (&x)[Geo<D, KP>::DH], const bf16x8 (&Aop)[Geo<D, KP>::KT][Geo<D, KP>::DS + 1],
+                                            const bf16x8 &Bone, f32x16 (&a)[Geo<D, KP>::KT]) {
+    using G = Geo<D, KP>;
+    bf16x8 B[G::DS];
+#pragma unroll
+    for (int s = 0; s < G::DS; s++)
+#pragma unroll
+        for (int q = 0; q < 8; q++) B[s][q] = (__bf16)x[8 * s + q];
+    const f32x16 zero = {};
+#pragma unroll
+    for (int t = 0; t < G::KT; t++) {
+        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][0], B[0], zero, 0, 0, 0);
+#pragma unroll
+        for (int s = 1; s < G::DS; s++) a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][s], B[s], a[t], 0, 0, 0);
+        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][G::DS], Bone, a[t], 0, 0, 0);
+    }
+}
+
+template <int D, int KP>
+__device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], float &m1, float &m2) {
+    using G = Geo<D, KP>;
+    constexpr uint32_t IMASK = (1u << G::IB) - 1u;
+    m1 = 3.4e38f;
+    m2 = 3.4e38f;
+#pragma unroll
+    for (int t = 0; t < G::KT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float key = f32((u32(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
+            m2 = __builtin_amdgcn_fmed3f(m1, m2, key);
+            m1 = fminf(m1, key);
+        }
+}
+
+// candidate bits of this lane's screen values against threshold T: bit (8(v/4) + 4h + v%4) of word t
+template <int D, int KP>
+__device__ __forceinline__ void cand_bits(const f32x16 (&a)[Geo<D, KP>::KT], float T, float rho, int h,
+                                          uint32_t (&w)[Geo<D, KP>::KT]) {
+    using G = Geo<D, KP>;
+    constexpr uint32_t IMASK = (1u << G::IB) - 1u;
+#pragma unroll
+    for (int t = 0; t < G::KT; t++) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float key = f32((u32(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
+            if (key - rho * fabsf(key) <= T) m |= 1u << (8 * (v >> 2) + 4 * h + (v & 3));
+        }
+        w[t] = m;
+    }
+}
+
+template <int D, int KP>
+__device__ __forceinline__ void load_half(const float *__restrict__ X, int64_t row, int h, float (&x)[Geo<D, KP>::DH]) {
+    using G = Geo<D, KP>;
+    static_assert(D == G::DP, "rows are loaded as whole float4s");
+    const float4 *src = reinterpret_cast<const float4 *>(X + row * D + h * G::DH);
+#pragma unroll
+    for (int q = 0; q < G::DH / 4; q++) {
+        const float4 v = src[q];
+        x[4 * q] = v.x;
+        x[4 * q + 1] = v.y;
+        x[4 * q + 2] = v.z;
+        x[4 * q + 3] = v.w;
+    }
+}
+
+// Split x into three bf16 pieces with x = hi + mid + lo exactly (truncation: hi keeps the top 8 significant
+// bits, mid the next 8 of the remainder, lo the rest, which has at most 8 significant bits), and pack pairs.
+__device__ __forceinline__ void split3(const float (&x)[8], bf16x8 &ph, bf16x8 &pm, bf16x8 &pl) {
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const float a = x[2 * p], b = x[2 * p + 1];
+        const float ra = a - f32(u32(a) & 0xffff0000u), rb = b - f32(u32(b) & 0xffff0000u);
+        const float sa = ra - f32(u32(ra) & 0xffff0000u), sb = rb - f32(u32(rb) & 0xffff0000u);
+        h[p] = __builtin_amdgcn_perm(u32(b), u32(a), 0x07060302u);
+        m[p] = __builtin_amdgcn_perm(u32(rb), u32(ra), 0x07060302u);
+        l[p] = __builtin_amdgcn_perm(u32(sb), u32(sa), 0x07060302u);
+    }
+    ph = *reinterpret_cast<bf16x8 *>(h);
+    pm = *reinterpret_cast<bf16x8 *>(m);
+    pl = *reinterpret_cast<bf16x8 *>(l);
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Rows reach LDS by direct global->LDS loads (global_load_lds_dwordx4), double-buffered one 64-row block
+// ahead. A block is two 32-row tiles; a tile of D floats per row is NC = D/4 16-byte chunks per row, loaded
+// by NC/2 instructions: instruction q puts chunk q of row ln in lane ln (lanes 0-31) and chunk NC/2+q of row
+// (ln ^ 4) in lane 32+ln. Instruction regions are 1040 bytes apart (1024 + a 16-byte pad). With this layout the
+// screen's half-row reads and the accumulation's transposed reads (one dim, eight rows per lane) both touch
+// distinct LDS banks.
+template <int D>
+struct Lay {
+    static constexpr int NC = D / 4;          // 16-byte chunks per row
+    static constexpr int QI = NC / 2;         // load instructions per tile
+    static constexpr int RB = 1040;           // bytes per instruction region
+    static constexpr int BUF = 2 * QI * RB;   // bytes per 64-row block
+};
+
+typedef __attribute__((address_space(3))) void *lds_vptr;
+typedef __attribute__((address_space(1))) void *gbl_vptr;
+
+// issue the loads of the 64-row block starting at r0 (rows past r_end read row r_end - 1; never used)
+template <int D>
+__device__ __forceinline__ void issue_block(const float *__restrict__ X, int64_t r0, int64_t r_end, int lane,
+                                            char *buf) {
+    using L = Lay<D>;
+    const int ln = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int tile = 0; tile < 2; tile++) {
+        const int rr = h ? (ln ^ 4) : ln;
+        int64_t row = r0 + 32 * tile + rr;
+        row = row < r_end ? row : r_end - 1;
+#pragma unroll
+        for (int q = 0; q < L::QI; q++) {
+            const float *src = X + row * D + 4 * (h * L::QI + q);
+            __builtin_amdgcn_global_load_lds((gbl_vptr)src, (lds_vptr)(buf + (tile * L::QI + q) * L::RB), 16, 0, 0);
+        }
+    }
+}
+
+// this lane's half row of tile `tile` (row ln, dims h*D/2 ..) from a loaded block
+template <int D>
+__device__ __forceinline__ void read_half(const char *buf, int tile, int lane, float (&x)[D / 2]) {
+    using L = Lay<D>;
+    const int ln = lane & 31, h = lane >> 5;
+    const int slot = h ? 32 + (ln ^ 4) : ln;
+#pragma unroll
+    for (int q = 0; q < L::QI; q++) {
+        const float4 v = *reinterpret_cast<const float4 *>(buf + (tile * L::QI + q) * L::RB + slot * 16);
+        x[4 * q] = v.x;
+        x[4 * q + 1] = v.y;
+        x[4 * q + 2] = v.z;
+        x[4 * q + 3] = v.w;
+    }
+}
+
+// x[row][dim] of a loaded block (row < 64, dim < D)
+template <int D>
+__device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
+    using L = Lay<D>;
+    const int tile = row >> 5, rr = row & 31, c = dim >> 2;
+    const int hp = c >= L::QI, q = hp ? c - L::QI : c;
+    const int slot = hp ? 32 + (rr ^ 4) : rr;
+    return *reinterpret_cast<const float *>(buf + (tile * L::QI + q) * L::RB + slot * 16 + (dim & 3) * 4);
+}
+
+template <int D, int KP, int WAVES, bool ACCUM>
+__global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
+    const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k, const float *__restrict__ maxes,
+    const uint16_t *__restrict__ cbg, int64_t rbs, uint32_t *__restrict__ labels, float *__restrict__ best,
+    float *__restrict__ psum, float *__restrict__ pcomp, int rb0, km_control *__restrict__ ctl,
+    const int32_t *__restrict__ stop) {
+    using G = Geo<D, KP>;
+    using L = Lay<D>;
+    constexpr int DH = G::DH, DS = G::DS, KT = G::KT, CS = G::CS, W = D + 2;
+    constexpr int NT = (D + 31) / 32;                 // 32-dim tiles of the accumulation
+    constexpr int FOLD = (KP * 32 * NT + 2 * KP) * 4; // bytes of the end-of-block fold per wave
+    // per wave: two block buffers + 64 uint16 labels during the loop, the fold after it
+    constexpr int WBYTES = (2 * L::BUF + 128 > FOLD) ? 2 * L::BUF + 128 : FOLD;
+    // window constants
+    constexpr float BETA = (float)(2.0 * (0x1p-8 + 0x1p-18) * (1.0 + 0x1p-20) + 2.01 * km_gamma(G::DP + 2));
+    constexpr float GAM2 = (float)(km_gamma(G::DP + 2) + 0x1p-17);
     constexpr float GDIR = (float)(km_gamma(D + 2) / (1.0 - km_gamma(D + 2)) * (1.0 + 0x1p-20));
-    constexpr float RHO = (float)(1.01 * (double)(1 << IB) * 0x1p-23);
-    constexpr float FLUSH = (float)(0x1p-123 * 16.0);   // bf16 denormal flush, times sqrt(DP) <= 16 below
-    constexpr float TINY = (float)(DP * 0x1p-118);
-    constexpr float XSQ_UP = (float)(1.0 + 2.0 * (DH + 2) * 0x1p-24);
-    static_assert(DP <= 64 && KP <= 128, "fused kernel serves dims <= 64 and k <= 128");
+    constexpr float RHO = (float)(1.01 * (double)(1 << G::IB) * 0x1p-23);
+    constexpr float FLUSH = (float)(0x1p-123 * 16.0);
+    constexpr float TINY = (float)((G::DP + 2) * 0x1p-118);
+    constexpr float XSQ_UP = (float)(1.0 + 2.0 * (D + 2) * 0x1p-24);
+    constexpr uint32_t IMASK = (1u << G::IB) - 1u;
+    static_assert(D == G::DP && D <= 64 && KP <= 128, "fused kernel serves dims 16, 32, 64 and k <= 128");
 
     if (stop && *stop) return;
 
     extern __shared__ float lds[];
-    float *Cl = lds;                                       // KP x CS float32 centres
+    float *Cl = lds;                                  // KP x CS float32 centres
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float *wbase = lds + KP * CS + wave * (KP * D * 2 + KP + 32 * D);
-    float2 *acc = reinterpret_cast<float2 *>(wbase);       // KP x D (sum, kahan carry)
-    uint32_t *cnt = reinterpret_cast<uint32_t *>(wbase + KP * D * 2);   // KP counts
-    float *TT = wbase + KP * D * 2 + KP;                   // 32 x D transpose tile
-
-    // centres into LDS (zeros for padding), accumulators cleared
-    for (int e = threadIdx.x; e < KP * CS; e += 64 * KM_WAVES) {
-        const int c = e / CS, j = e % CS;
-        Cl[e] = (c < k && j < D) ? C[(size_t)c * D + j] : 0.0f;
-    }
-    if (ACCUM) {
-        for (int e = lane; e < KP * D; e += 64) acc[e] = make_float2(0.0f, 0.0f);
-        for (int e = lane; e < KP; e += 64) cnt[e] = 0u;
-    }
-
-    const int rn = lane & 31, h = lane >> 5;
-    // resident MFMA operands: A = bf16(-2c) per (tile, k-step); C = |c|^2 of this lane's 16 centres per tile
-    bf16x8 Aop[KT][DS];
-#pragma unroll
-    for (int t = 0; t < KT; t++)
-#pragma unroll
-        for (int s = 0; s < DS; s++)
-            Aop[t][s] = *reinterpret_cast<const bf16x8 *>(cbg + ((size_t)(t * DS + s) * 64 + lane) * 8);
-    f32x16 Cin[KT];
-#pragma unroll
-    for (int t = 0; t < KT; t++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) Cin[t][v] = csq[32 * t + 8 * (v >> 2) + 4 * h + (v & 3)];
-    const float cnmax = maxes[0], csqmax = maxes[1];
-    __syncthreads();
+    char *wbase = reinterpret_cast<char *>(lds + KP * CS) + wave * WBYTES;
+    char *bufs[2] = {wbase, wbase + L::BUF};
+    uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * L::BUF);   // labels of the block (0x4000: no row)
 
     const int64_t r_begin = (int64_t)blockIdx.x * rbs;
     const int64_t r_end = (r_begin + rbs < n) ? r_begin + rbs : n;
-    float ine_s = 0.0f, ine_c = 0.0f;   // this lane's Kahan inertia (half 1 lanes)
-    uint32_t fallback = 0;              // rows of this lane's tiles rescored against every centre
+    int64_t r0 = r_begin + (int64_t)wave * 64;
+    if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, bufs[0]);
 
-    for (int64_t r0 = r_begin + (int64_t)wave * 32; r0 < r_end; r0 += 32 * KM_WAVES) {
-        const int64_t row = r0 + rn;
-        const bool valid = row < r_end;
-        // ---- load this lane's half row
-        float xf[DH];
-        if (D == DP) {   // whole float4s: 16-byte aligned rows (checked by the host)
-            const float4 *src = reinterpret_cast<const float4 *>(X + row * D + h * DH);
+    for (int e = threadIdx.x; e < KP * CS; e += 64 * WAVES) {
+        const int c = e / CS, j = e % CS;
+        Cl[e] = (c < k && j < D) ? C[(size_t)c * D + j] : 0.0f;
+    }
+    const int h = lane >> 5, ln = lane & 31;
+    bf16x8 Aop[KT][DS + 1];
 #pragma unroll
-            for (int q = 0; q < DH / 4; q++) {
-                const float4 v = valid ? src[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                xf[4 * q] = v.x;
-                xf[4 * q + 1] = v.y;
-                xf[4 * q + 2] = v.z;
-                xf[4 * q + 3] = v.w;
-            }
+    for (int t = 0; t < KT; t++)
+#pragma unroll
+        for (int s = 0; s <= DS; s++)
+            Aop[t][s] = *reinterpret_cast<const bf16x8 *>(cbg + ((size_t)(t * (DS + 1) + s) * 64 + lane) * 8);
+    bf16x8 Bone;
+#pragma unroll
+    for (int q = 0; q < 8; q++) Bone[q] = (__bf16)((h == 0 && q < 2) ? 1.0f : 0.0f);
+    const float cnmax = maxes[0], csqmax = maxes[1];
+    __syncthreads();
+
+    float ine_s = 0.0f, ine_c = 0.0f;   // Kahan inertia of this lane's rows
+    uint32_t fallback = 0;
+    f32x16 sacc[KT][NT];
+#pragma unroll
+    for (int t = 0; t < KT; t++)
+#pragma unroll
+        for (int u = 0; u < NT; u++) sacc[t][u] = f32x16{};
+    uint32_t nomatch[KT];     // rows compared by this lane whose label is not centre 32t + ln
+#pragma unroll
+    for (int t = 0; t < KT; t++) nomatch[t] = 0;
+    uint32_t rows_seen = 0;   // rows this lane compared
+    const uint32_t ones = 0x00010001u, c3f80 = 0x3f803f80u, cneg = 0xc080c080u;
+
+    int cur = 0;
+    for (; r0 < r_end; r0 += 64 * WAVES, cur ^= 1) {
+        const char *buf = bufs[cur];
+        // ---- prefetch the next block into the other buffer, then wait for this one
+        const int64_t r1 = r0 + 64 * WAVES;
+        if (r1 < r_end) {
+            issue_block<D>(X, r1, r_end, lane, bufs[cur ^ 1]);
+            if (L::QI == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else if (L::QI == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         } else {
-#pragma unroll
-            for (int q = 0; q < DH; q++) {
-                const int j = h * DH + q;
-                xf[q] = (valid && j < D) ? X[row * D + j] : 0.0f;
-            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        // ---- |x|^2 upper bound and |x| upper bound
-        float xs = 0.0f;
+        const int64_t row = r0 + lane;     // the row this lane owns after the exchange
+        const bool valid = row < r_end;
+        float xa[DH], xb[DH];
+        read_half<D>(buf, 0, lane, xa);
+        read_half<D>(buf, 1, lane, xb);
+        // ---- screens of tiles A and B
+        float sa = 0.0f, sb = 0.0f;
 #pragma unroll
-        for (int q = 0; q < DH; q++) xs = __builtin_fmaf(xf[q], xf[q], xs);
-        const float xsq_up = (xs + shfl32(xs)) * XSQ_UP;
-        const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
-        // ---- screen on the matrix cores
-        bf16x8 B[DS];
-#pragma unroll
-        for (int s = 0; s < DS; s++)
-#pragma unroll
-            for (int q = 0; q < 8; q++) B[s][q] = (__bf16)xf[8 * s + q];
-        f32x16 a[KT];
-#pragma unroll
-        for (int t = 0; t < KT; t++) {
-            a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][0], B[0], Cin[t], 0, 0, 0);
-#pragma unroll
-            for (int s = 1; s < DS; s++) a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][s], B[s], a[t], 0, 0, 0);
+        for (int q = 0; q < DH; q++) {
+            sa = __builtin_fmaf(xa[q], xa[q], sa);
+            sb = __builtin_fmaf(xb[q], xb[q], sb);
         }
-        // ---- smallest and second smallest screen value, with the local index packed into the low bits
-        const uint32_t IMASK = (1u << IB) - 1u;
-        float m1 = 3.4e38f, m2 = 3.4e38f;
-#pragma unroll
-        for (int t = 0; t < KT; t++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const float key = __uint_as_float((__float_as_uint(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
-                m2 = __builtin_amdgcn_fmed3f(m1, m2, key);
-                m1 = fminf(m1, key);
-            }
-        const float pm1 = shfl32(m1), pm2 = shfl32(m2);
-        const float km = fminf(m1, pm1);
-        const float k2 = fminf(fmaxf(m1, pm1), fminf(m2, pm2));
-        // index of km: which half holds it, and where
-        const uint32_t kmb = __float_as_uint(km) & IMASK;
-        const int kh = (m1 == pm1) ? 0 : ((km == m1) ? h : (h ^ 1));   // equal keys: half 0's (either is fine)
+        float m1a, m2a, m1b, m2b;
+        {
+            f32x16 a[KT];
+            screen_tile<D, KP>(xa, Aop, Bone, a);
+            min2_keys<D, KP>(a, m1a, m2a);
+        }
+        {
+            f32x16 a[KT];
+            screen_tile<D, KP>(xb, Aop, Bone, a);
+            min2_keys<D, KP>(a, m1b, m2b);
+        }
+        // ---- the owned row's two halves
+        float p0, p1, q0, q1, s0, s1;
+        own_halves(m1a, m1b, p0, p1);
+        own_halves(m2a, m2b, q0, q1);
+        own_halves(sa, sb, s0, s1);
+        const float km = fminf(p0, p1);
+        const int kh = (p0 <= p1) ? 0 : 1;
+        const float k2 = fminf(fmaxf(p0, p1), fminf(q0, q1));
+        const uint32_t kmb = u32(km) & IMASK;
         const int kt = (int)kmb >> 4, kv = (int)kmb & 15;
         const int cm = 32 * kt + 8 * (kv >> 2) + 4 * kh + (kv & 3);
-        // ---- window
+        const float xsq_up = (s0 + s1) * XSQ_UP;
+        const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
         const float E = BETA * nx * cnmax + GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
         const float akm = km + RHO * fabsf(km);
         const float dm_up = fmaxf(0.0f, xsq_up + akm + E) * (1.0f + 0x1p-20f);
-        const float margin = (2.0f * E + 2.0f * GDIR * dm_up) * (1.0f + 0x1p-20f) + TINY;
-        float T = akm + margin;
+        float T = akm + ((2.0f * E + 2.0f * GDIR * dm_up) * (1.0f + 0x1p-20f) + TINY);
         T = T + 0x1p-22f * fabsf(T);
         const bool unique = (k2 - RHO * fabsf(k2)) > T && cm < k;
-        // ---- candidate masks (one 32-bit word per centre tile, bit = centre within the tile)
         uint32_t mw[KT];
 #pragma unroll
-        for (int t = 0; t < KT; t++) mw[t] = (t == kt) ? (1u << (cm & 31)) : 0u;
-        const bool any_multi = __ballot(!unique && valid) != 0;
-        if (any_multi) {
-            uint32_t own_w[KT];
-#pragma unroll
-            for (int t = 0; t < KT; t++) {
-                uint32_t wv = 0;
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const float key = __uint_as_float((__float_as_uint(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
-                    if (key - RHO * fabsf(key) <= T) wv |= 1u << (8 * (v >> 2) + 4 * h + (v & 3));
-                }
-                own_w[t] = wv;
+        for (int t = 0; t < KT; t++) mw[t] = (t == kt && cm < k) ? (1u << (cm & 31)) : 0u;
+        // ---- rows the screen cannot settle alone: every centre inside the window (rare)
+        if (__ballot(!unique && valid) != 0) {
+            asm volatile("" ::: "memory");   // the re-reads below stay inside this branch
+            float ya[DH], yb[DH];
+            read_half<D>(buf, 0, lane, ya);
+            read_half<D>(buf, 1, lane, yb);
+            const float Tp = partner(T, lane);
+            const float TA = (lane < 32) ? T : Tp, TB = (lane < 32) ? Tp : T;
+            uint32_t wa[KT], wb[KT];
+            {
+                f32x16 a[KT];
+                screen_tile<D, KP>(ya, Aop, Bone, a);
+                cand_bits<D, KP>(a, TA, RHO, h, wa);
+            }
+            {
+                f32x16 a[KT];
+                screen_tile<D, KP>(yb, Aop, Bone, a);
+                cand_bits<D, KP>(a, TB, RHO, h, wb);
             }
 #pragma unroll
             for (int t = 0; t < KT; t++) {
-                uint32_t u = own_w[t] | shfl32u(own_w[t]);
-                // only real centres
+                uint32_t u0, u1;
+                own_halves_u(wa[t], wb[t], u0, u1);
+                uint32_t u = u0 | u1;
                 const int lim = k - 32 * t;
                 if (lim < 32) u &= lim <= 0 ? 0u : ((1u << lim) - 1u);
                 if (!unique) mw[t] = u;
             }
-        }
-        bool full = false;
-        {
             uint32_t any = 0;
 #pragma unroll
             for (int t = 0; t < KT; t++) any |= mw[t];
-            full = (any == 0);   // nothing usable (non-finite data): score every centre
+            if (any == 0) {   // nothing finite in the window (non-finite data): score every centre
+#pragma unroll
+                for (int t = 0; t < KT; t++) {
+                    const int lim = k - 32 * t;
+                    mw[t] = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+                }
+            }
         }
-        if (full) {
+        // ---- every lane takes its whole row
+        float lo[DH], hi[DH];
+#pragma unroll
+        for (int q = 0; q < DH; q++) own_halves(xa[q], xb[q], lo[q], hi[q]);
+        // ---- exact rescoring: the lowest candidate, then (rare) the others in ascending order, strict '<'
+        int c0 = 0;
+        {
+            bool got = false;
+#pragma unroll
+            for (int t = 0; t < KT; t++)
+                if (!got && mw[t]) {
+                    c0 = 32 * t + __builtin_ctz(mw[t]);
+                    got = true;
+                }
+        }
+        float bst;
+        uint32_t bl = (uint32_t)c0;
+        {
+            const float *cc = Cl + c0 * CS;
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < DH; q++) { const float t = lo[q] - cc[q]; s = s + t * t; }
+#pragma unroll
+            for (int q = 0; q < DH; q++) { const float t = hi[q] - cc[DH + q]; s = s + t * t; }
+            bst = s;
+            // the rows loop keeps best = INFINITY and label 0 when no distance compares below it (NaN)
+            if (!(s < INFINITY)) { bst = INFINITY; bl = 0; }
+        }
+        if (!unique) {
+            asm volatile("" ::: "memory");
+            mw[c0 >> 5] &= ~(1u << (c0 & 31));
+            fallback += valid ? 1u : 0u;
 #pragma unroll
             for (int t = 0; t < KT; t++) {
-                const int lim = k - 32 * t;
-                mw[t] = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
-            }
-        }
-        // ---- exact rescoring of the candidates, ascending centre index, strict '<' (the rows loop)
-        float bst = INFINITY;
-        uint32_t bl = 0;
-        uint32_t ncand = 0;
-#pragma unroll
-        for (int t = 0; t < KT; t++) {
-            uint32_t wv = mw[t];
-            while (wv) {
-                const int b = __builtin_ctz(wv);
-                wv &= wv - 1u;
-                const int c = 32 * t + b;
-                const float *cc = Cl + c * CS;
-                float s = 0.0f;
-                if (h == 0) {
-#pragma unroll
-                    for (int q = 0; q < DH; q++) {
-                        if (q < D) {
-                            const float tq = xf[q] - cc[q];
-                            s = s + tq * tq;
-                        }
-                    }
-                }
-                const float s0 = shfl32(s);
-                if (h == 1) {
-                    s = s0;
-#pragma unroll
-                    for (int q = 0; q < DH; q++) {
-                        if (DH + q < D) {
-                            const float tq = xf[q] - cc[DH + q];
-                            s = s + tq * tq;
-                        }
-                    }
+                uint32_t wv = mw[t];
+                while (wv) {
+                    const int b = __builtin_ctz(wv);
+                    wv &= wv - 1u;
+                    const int c = 32 * t + b;
+                    const float *cc = Cl + c * CS;
+                    float s = 0.0f;
+                    for (int q = 0; q < DH; q++) { const float tq = lo[q] - cc[q]; s = s + tq * tq; }
+                    for (int q = 0; q < DH; q++) { const float tq = hi[q] - cc[DH + q]; s = s + tq * tq; }
                     if (s < bst) { bst = s; bl = (uint32_t)c; }
                 }
-                ncand++;
             }
         }
-        // the result lives in half 1; give it to half 0 too
-        {
-            const float ob = shfl32(bst);
-            const uint32_t ol = shfl32u(bl);
-            if (h == 0) { bst = ob; bl = ol; }
-        }
-        if (h == 1 && valid && ncand > 1) fallback++;
-        if (valid && h == 1) {
+        if (valid) {
             if (labels) labels[row] = bl;
             if (best) best[row] = bst;
         }
-        if (!ACCUM) continue;
-        // ---- accumulation
-        if (valid && h == 1) {
-            atomicAdd(&cnt[bl], 1u);
-            const float y = bst - ine_c;
-            const float tt = ine_s + y;
-            ine_c = (tt - ine_s) - y;
-            ine_s = tt;
-        }
-#pragma unroll
-        for (int q = 0; q < DH; q++)
-            if (h * DH + q < D) TT[rn * D + h * DH + q] = xf[q];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const uint32_t lab_mine = valid ? bl : 0xffffffffu;
-        const int half = lane >> 5, j = lane & 31;
-        for (int i = 0; i < 16; i++) {
-            const uint32_t L0 = __builtin_amdgcn_readlane(lab_mine, 2 * i);
-            const uint32_t L1 = __builtin_amdgcn_readlane(lab_mine, 2 * i + 1);
-            if (L0 == 0xffffffffu) break;   // rows past the end come last in a tile
-            const uint32_t L = half ? L1 : L0;
-            const bool act = (half == 0 || L1 != 0xffffffffu) && j < D;   // D < 32: lanes past D idle
-#define KM_KAHAN_UPD()                                              \
-    for (int jj = j; jj < D; jj += 32) {                            \
-        const float xv = TT[(2 * i + half) * D + jj];               \
-        float2 sc = acc[L * D + jj];                                \
-        const float y = xv - sc.y;                                  \
-        const float tt = sc.x + y;                                  \
-        sc.y = (tt - sc.x) - y;                                     \
-        sc.x = tt;                                                  \
-        acc[L * D + jj] = sc;                                       \
-    }
-            if (L0 != L1) {
-                if (act) KM_KAHAN_UPD();
-            } else {
-                if (act && half == 0) KM_KAHAN_UPD();
-                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                if (act && half == 1) KM_KAHAN_UPD();
+        if (ACCUM) {
+            // ---- accumulation on the matrix cores: sums (centres x dims) += onehot^T (centres x rows) x rows
+            if (valid) {
+                const float y = bst - ine_c;
+                const float tt = ine_s + y;
+                ine_c = (tt - ine_s) - y;
+                ine_s = tt;
             }
-#undef KM_KAHAN_UPD
+            L16[lane] = valid ? (uint16_t)bl : (uint16_t)0x4000u;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            uint32_t miss[KT];   // per 16-bit half, at most 16 per block
+#pragma unroll
+            for (int t = 0; t < KT; t++) miss[t] = 0;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int rbase = 16 * ks + 8 * h;           // this lane's 8 rows of the K-step
+                const uint4 lp = *reinterpret_cast<const uint4 *>(L16 + rbase);   // 8 uint16 labels
+                const uint32_t lab2[4] = {lp.x, lp.y, lp.z, lp.w};
+                bf16x8 OH[KT];
+#pragma unroll
+                for (int t = 0; t < KT; t++) {
+                    const uint32_t mm = (uint32_t)(32 * t + ln) * 0x00010001u;
+                    uint32_t o[4];
+#pragma unroll
+                    for (int p = 0; p < 4; p++) {
+                        // per 16-bit half: y = min(label ^ m, 1) is 0 exactly on a match; onehot = 0x3f80 - y * 0x3f80
+                        uint32_t y, oh;
+                        asm("v_pk_min_u16 %0, %1, %2" : "=v"(y) : "v"(lab2[p] ^ mm), "v"(ones));
+                        asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(oh) : "v"(y), "v"(cneg), "v"(c3f80));
+                        asm("v_pk_add_u16 %0, %1, %2" : "=v"(miss[t]) : "v"(miss[t]), "v"(y));
+                        o[p] = oh;
+                    }
+                    OH[t] = *reinterpret_cast<bf16x8 *>(o);
+                }
+#pragma unroll
+                for (int u = 0; u < NT; u++) {
+                    float xv[8];
+                    const int col = 32 * u + ln;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) xv[i] = (col < D) ? read_elem<D>(buf, rbase + i, col) : 0.0f;
+                    bf16x8 ph, pm, pl;
+                    split3(xv, ph, pm, pl);
+#pragma unroll
+                    for (int t = 0; t < KT; t++) {
+                        sacc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], ph, sacc[t][u], 0, 0, 0);
+                        sacc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], pm, sacc[t][u], 0, 0, 0);
+                        sacc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], pl, sacc[t][u], 0, 0, 0);
+                    }
+                }
+            }
+            rows_seen += 32;
+#pragma unroll
+            for (int t = 0; t < KT; t++) nomatch[t] += (miss[t] & 0xffffu) + (miss[t] >> 16);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     if (fallback) atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)fallback);
     if (!ACCUM) return;
 
-    // ---- fold the waves' accumulators in wave order and write this block's partial
-    // inertia: fixed-order reduction of the lanes' (s, c), then waves in order
-    __shared__ float ine_w[KM_WAVES * 2];
+    // ---- fold: each wave leaves its sums and counts in its own buffers; the block folds them in wave order
+    __shared__ float ine_w[WAVES * 2];
     {
-        float s = (h == 1) ? ine_s : 0.0f;
-        float c = (h == 1) ? -ine_c : 0.0f;   // Kahan carry c means the true sum is s - c
+        float s = ine_s, c = -ine_c;   // Kahan: the true sum is s - carry
         for (int off = 32; off > 0; off >>= 1) {
             const float so = __shfl_xor(s, off), co = __shfl_xor(c, off);
-            // combine in lane order: lower half first
             const float a0 = (lane & off) ? so : s, a1 = (lane & off) ? s : so;
             const float c0 = (lane & off) ? co : c, c1 = (lane & off) ? c : co;
             const float tt = a0 + a1;
@@ -406,36 +625,51 @@ __global__ __launch_bounds__(64 * KM_WAVES) void k_fused_mfma(
             ine_w[wave * 2 + 1] = c;
         }
     }
+    float *F = reinterpret_cast<float *>(wbase);                      // KP x (32 NT) sums of this wave
+    uint32_t *FC = reinterpret_cast<uint32_t *>(F + KP * 32 * NT);    // 2 x KP match counts (one per half)
+#pragma unroll
+    for (int t = 0; t < KT; t++)
+#pragma unroll
+        for (int u = 0; u < NT; u++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int c = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+                F[c * (32 * NT) + 32 * u + ln] = sacc[t][u][v];
+            }
+#pragma unroll
+    for (int t = 0; t < KT; t++)   // rows of this lane labelled 32t + ln
+        FC[h * KP + 32 * t + ln] = rows_seen - nomatch[t];
     __syncthreads();
     const int64_t kw = (int64_t)k * W;
     float *ps = psum + (int64_t)(rb0 + blockIdx.x) * kw;
     float *pc = pcomp + (int64_t)(rb0 + blockIdx.x) * kw;
-    for (int e = threadIdx.x; e < k * W; e += 64 * KM_WAVES) {
+    const char *base = reinterpret_cast<const char *>(lds + KP * CS);
+    for (int e = threadIdx.x; e < k * W; e += 64 * WAVES) {
         const int c = e / W, col = e % W;
         float s = 0.0f, cc = 0.0f;
         if (col == 0) {
             uint32_t tot = 0;
-            for (int w = 0; w < KM_WAVES; w++)
-                tot += reinterpret_cast<const uint32_t *>(lds + KP * CS + w * (KP * D * 2 + KP + 32 * D) + KP * D * 2)[c];
+            for (int w = 0; w < WAVES; w++) {
+                const uint32_t *fcw = reinterpret_cast<const uint32_t *>(base + w * WBYTES) + KP * 32 * NT;
+                tot += fcw[c] + fcw[KP + c];
+            }
             s = (float)tot;
         } else if (col == 1) {
             if (c == 0) {
-                for (int w = 0; w < KM_WAVES; w++) {
-                    const float v = ine_w[2 * w], vc = ine_w[2 * w + 1];
+                for (int w = 0; w < WAVES; w++) {
+                    const float v = ine_w[2 * w];
                     const float tt = s + v;
                     cc += (fabsf(s) >= fabsf(v)) ? ((s - tt) + v) : ((v - tt) + s);
-                    cc += vc;
+                    cc += ine_w[2 * w + 1];
                     s = tt;
                 }
             }
         } else {
             const int jj = col - 2;
-            for (int w = 0; w < KM_WAVES; w++) {
-                const float2 sc = reinterpret_cast<const float2 *>(lds + KP * CS + w * (KP * D * 2 + KP + 32 * D))[c * D + jj];
-                const float v = sc.x, vc = -sc.y;   // Kahan: true = x - carry
+            for (int w = 0; w < WAVES; w++) {
+                const float v = reinterpret_cast<const float *>(base + w * WBYTES)[c * (32 * NT) + jj];
                 const float tt = s + v;
                 cc += (fabsf(s) >= fabsf(v)) ? ((s - tt) + v) : ((v - tt) + s);
-                cc += vc;
                 s = tt;
             }
         }
@@ -446,40 +680,36 @@ __global__ __launch_bounds__(64 * KM_WAVES) void k_fused_mfma(
 
 // ------------------------------------------------------------------ planning and launch
 
-template <int D, int KP, bool ACCUM>
-static size_t fused_lds() {
-    constexpr int CS = D + 4;
-    return (size_t)(KP * CS + KM_WAVES * (KP * D * 2 + KP + 32 * D)) * sizeof(float);
-}
+typedef void (*fused_fn)(const float *, int64_t, const float *, int, const float *, const uint16_t *, int64_t,
+                         uint32_t *, float *, float *, float *, int, km_control *, const int32_t *);
 
-typedef void (*fused_fn)(const float *, int64_t, const float *, int, const float *, const float *, const uint16_t *,
-                         int64_t, uint32_t *, float *, float *, float *, int, km_control *, const int32_t *);
-
+// One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
 struct fused_entry {
     int d, kp;
-    fused_fn acc, noacc;
-    size_t lds;
+    fused_fn acc4, noacc4, acc2, noacc2;
 };
 
-#define KM_FUSED(DD, KK) \
-    {DD, KK, k_fused_mfma<DD, KK, true>, k_fused_mfma<DD, KK, false>, 0}
+#define KM_FUSED(DD, KK)                                                                             \
+    {DD, KK, k_fused_mfma<DD, KK, 4, true>, k_fused_mfma<DD, KK, 4, false>, k_fused_mfma<DD, KK, 2, true>, \
+     k_fused_mfma<DD, KK, 2, false>}
 
 static fused_entry g_fused[] = {
-    KM_FUSED(16, 32), KM_FUSED(16, 64), KM_FUSED(16, 128),
+    KM_FUSED(16, 32), KM_FUSED(16, 64),
     KM_FUSED(32, 32), KM_FUSED(32, 64),
     KM_FUSED(64, 32),
 };
 #undef KM_FUSED
 
-static size_t lds_for(int d, int kp) {
-    return (size_t)(kp * (d + 4) + KM_WAVES * (kp * d * 2 + kp + 32 * d)) * sizeof(float);
+static size_t lds_for(int d, int kp, int waves) {
+    const size_t loop = 2 * (size_t)(2 * (d / 8) * 1040) + 128;   // two block buffers + labels
+    const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float);
+    return (size_t)kp * (d + 4) * sizeof(float) + waves * (loop > fold ? loop : fold);
 }
 
 static const fused_entry *find_fused(int d, int k) {
-    const int kp = (k + 31) / 32 * 32;
+    const int kp = k <= 32 ? 32 : k <= 64 ? 64 : k <= 128 ? 128 : 0;
     for (auto &e : g_fused)
-        if (e.d == d && e.kp >= kp && (e.kp == kp || (kp <= 32 ? e.kp == 32 : kp <= 64 ? e.kp == 64 : e.kp == 128)))
-            return &e;
+        if (e.d == d && e.kp == kp) return &e;
     return nullptr;
 }
 
@@ -491,33 +721,44 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused) {
     km_mfma_plan pl{};
     const fused_entry *fe = find_fused(d, k);
     if (!fe || n < 1) return pl;
-    pl.ok = 1;
-    pl.kpad = fe->kp;
-    pl.dpad = (d + 15) / 16 * 16;
-    pl.lds = lds_for(d, fe->kp);
     if (g_cus == 0) {
         int dev = 0;
         hipDeviceProp_t prop;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess) {
             g_cus = prop.multiProcessorCount;
+            g_lds_max = (size_t)prop.sharedMemPerBlock;
+        }
         if (g_cus <= 0) g_cus = 256;
-        g_lds_max = (size_t)prop.sharedMemPerBlock;
         if (g_lds_max == 0) g_lds_max = 65536;
     }
-    if (pl.lds > g_lds_max) {
-        pl.ok = 0;
-        return pl;
+    int waves = 4;
+    size_t lds = lds_for(d, fe->kp, 4);
+    if (lds > g_lds_max) {
+        waves = 2;
+        lds = lds_for(d, fe->kp, 2);
+        if (lds > g_lds_max) return pl;
+    }
+    fused_fn fn = waves == 4 ? fe->acc4 : fe->acc2;
+    if (lds > 65536) {
+        (void)hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipFuncSetAttribute((const void *)(waves == 4 ? fe->noacc4 : fe->noacc2),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)fe->acc, 64 * KM_WAVES, pl.lds) != hipSuccess ||
-        occ < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)fn, 64 * waves, lds) != hipSuccess || occ < 1)
         occ = 1;
+    pl.ok = 1;
+    pl.kpad = fe->kp;
+    pl.dpad = (d + 15) / 16 * 16;
+    pl.lds = lds;
+    pl.waves = waves;
     const int64_t slots = (int64_t)g_cus * occ;
-    const int64_t tiles = (n + 63) / 64;   // 64-row units (one per wave pair step)
-    int64_t nrb = tiles < slots ? tiles : slots;
+    const int64_t unit = 64 * waves;
+    const int64_t units = (n + unit - 1) / unit;
+    int64_t nrb = units < slots ? units : slots;
     if (nrb < 1) nrb = 1;
     int64_t rbs = (n + nrb - 1) / nrb;
-    rbs = (rbs + 63) / 64 * 64;
+    rbs = (rbs + unit - 1) / unit * unit;
     pl.rbs = rbs;
     pl.nrb = (int)((n + rbs - 1) / rbs);
     return pl;
@@ -528,8 +769,8 @@ hipError_t km_launch_mfma(const km_mfma_plan &pl, int fused, const float *X, int
                           km_control *ctl, const int32_t *stop, hipStream_t s) {
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
-    fused_fn fn = fused ? fe->acc : fe->noacc;
-    hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * KM_WAVES), pl.lds, s, X, n, C, k, aux.csq, aux.maxes, aux.cb, pl.rbs,
+    fused_fn fn = pl.waves == 4 ? (fused ? fe->acc4 : fe->noacc4) : (fused ? fe->acc2 : fe->noacc2);
+    hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, aux.maxes, aux.cb, pl.rbs,
                        labels, best, psum, pcomp, rb0, ctl, stop);
     return hipGetLastError();
 }
