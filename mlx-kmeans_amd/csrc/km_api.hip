@@ -71,6 +71,7 @@ struct km_ctx {
     DBuf<float> psum, pcomp;
     DBuf<double> tot;
     DBuf<double> tot2;      // (k, 2) [count, best] totals recomputed for km_pass on the fused path
+    DBuf<double> red;       // stage-1 sums of the reduce
     DBuf<uint32_t> labels;
     DBuf<float> best;
     km_control *ctl = nullptr;    // device
@@ -184,6 +185,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->pcomp.release();
     c->tot.release();
     c->tot2.release();
+    c->red.release();
     c->labels.release();
     c->best.release();
     for (auto &r : c->recs) {
@@ -283,6 +285,7 @@ static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bo
     HIPCHK(c, c->psum.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->tot.ensure((size_t)kw));
+    HIPCHK(c, c->red.ensure(km_reduce_tmp_doubles((int)total_rb, kw)));
     if (need_rows_scratch) {
         HIPCHK(c, c->labels.ensure((size_t)c->n));
         HIPCHK(c, c->best.ensure((size_t)c->n));
@@ -342,7 +345,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->tot.p, stop, c->stream); }));
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->red.p, c->tot.p, stop, c->stream); }));
         return KM_OK;
     }
 
@@ -371,7 +374,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         rb += plans[i].nrb;
         row0 += p.rows;
     }
-    HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->tot.p, stop, c->stream); }));
+    HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->red.p, c->tot.p, stop, c->stream); }));
     return KM_OK;
 }
 
@@ -439,6 +442,7 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
         HIPCHK(c, c->psum.ensure(total_rb * (size_t)k * 2));
         HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)k * 2));
         HIPCHK(c, c->tot2.ensure((size_t)k * 2));
+        HIPCHK(c, c->red.ensure(km_reduce_tmp_doubles((int)total_rb, (int64_t)k * 2)));
         int rb = 0;
         int64_t row0 = 0;
         for (size_t i = 0; i < c->parts.size(); i++) {
@@ -450,7 +454,7 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, c->tot2.p, nullptr, c->stream); }));
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, c->red.p, c->tot2.p, nullptr, c->stream); }));
         cb2.resize((size_t)k * 2);
         HIPCHK(c, hipMemcpyAsync(cb2.data(), c->tot2.p, cb2.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
     }

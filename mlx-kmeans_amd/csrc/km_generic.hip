@@ -210,22 +210,49 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
 }
 
 // ------------------------------------------------------------------ partials -> float64 totals
+//
+// Two stages, both in fixed order: stage 1 splits the row-blocks into KM_RED_SPLIT contiguous ranges and sums
+// each range per slot in float64; stage 2 adds the ranges in order. The partition depends only on the number of
+// row-blocks, so the result is the same on every run.
 
-__global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ psum, const float *__restrict__ pcomp,
-                                                int nrb, int64_t kw, double *__restrict__ tot,
-                                                const int32_t *__restrict__ stop) {
+static constexpr int KM_RED_SPLIT = 64;
+
+__global__ __launch_bounds__(256) void k_reduce1(const float *__restrict__ psum, const float *__restrict__ pcomp,
+                                                 int nrb, int64_t kw, int split, double *__restrict__ tmp,
+                                                 const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= kw) return;
-    double s = 0.0;
-    for (int r = 0; r < nrb; r++) s += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
-    tot[e] = s;
+    const int s = blockIdx.y;
+    const int r0 = (int)((int64_t)nrb * s / split), r1 = (int)((int64_t)nrb * (s + 1) / split);
+    double acc = 0.0;
+    for (int r = r0; r < r1; r++) acc += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
+    tmp[(int64_t)s * kw + e] = acc;
 }
 
-hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tot,
+__global__ __launch_bounds__(256) void k_reduce2(const double *__restrict__ tmp, int64_t kw, int split,
+                                                 double *__restrict__ tot, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= kw) return;
+    double acc = 0.0;
+    for (int s = 0; s < split; s++) acc += tmp[(int64_t)s * kw + e];
+    tot[e] = acc;
+}
+
+size_t km_reduce_tmp_doubles(int nrb, int64_t kw) {
+    const int split = nrb < KM_RED_SPLIT ? nrb : KM_RED_SPLIT;
+    return (size_t)split * kw;
+}
+
+hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tmp, double *tot,
                             const int32_t *stop, hipStream_t s) {
-    dim3 grid((unsigned)((kw + 255) / 256)), block(256);
-    hipLaunchKernelGGL(k_reduce, grid, block, 0, s, psum, pcomp, nrb, kw, tot, stop);
+    const int split = nrb < KM_RED_SPLIT ? (nrb < 1 ? 1 : nrb) : KM_RED_SPLIT;
+    const unsigned gx = (unsigned)((kw + 255) / 256);
+    hipLaunchKernelGGL(k_reduce1, dim3(gx, split), dim3(256), 0, s, psum, pcomp, nrb, kw, split, tmp, stop);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_reduce2, dim3(gx), dim3(256), 0, s, tmp, kw, split, tot, stop);
     return hipGetLastError();
 }
 

@@ -61,8 +61,9 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
                                    const uint32_t *labels, const float *best, int k, float *psum,
                                    float *pcomp, int rb0, const int32_t *stop, hipStream_t s);
 
-// Partials (nrb, k*w) sum+comp -> totals (k*w) float64, summed in row-block order.
-hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tot,
+// Partials (nrb, k*w) sum+comp -> totals (k*w) float64 in a fixed order; tmp holds km_reduce_tmp_doubles.
+size_t km_reduce_tmp_doubles(int nrb, int64_t kw);
+hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tmp, double *tot,
                             const int32_t *stop, hipStream_t s);
 
 // Update stage. stats: counts, inertia, empties, argmax, tol test; centres: C <- sums / counts.
