@@ -41,12 +41,16 @@ def log(*a):
 
 
 def profile_summary(name):
-    """HBM traffic per launch from a committed rocprofv3 --pmc summary, if one exists for this workload."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary for this
+    workload (FETCH_SIZE + WRITE_SIZE, each calibrated on a plain copy), or None if there is none."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
 
 
 def cpu_baseline(X, C, budget_s=12.0):

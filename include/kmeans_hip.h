@@ -99,7 +99,8 @@ int32_t km_profile_read(km_ctx *ctx, int32_t kernel, double *ms_total, int64_t *
 const char *km_kernel_name(int32_t kernel);
 
 /* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS or KM_PATH_MFMA), and the number of
- * rows the MFMA screen could not settle alone (rescored against every centre) in that pass. */
+ * rows in that pass that the MFMA screen could not settle alone: rows with more than one centre inside the
+ * screen's error window, each rescored with the direct form against every centre in its window. */
 int32_t km_last_path(const km_ctx *ctx);
 int64_t km_last_fallback_rows(km_ctx *ctx);
 

@@ -14,20 +14,19 @@
 // lane half h; the A operand (centres) is laid out with the same map, so the contraction runs over every dim.
 // Accumulator element v (0..15) of tile t in lane l is centre 32t + 8(v/4) + 4h + (v%4) against row n.
 //
-// Accumulation (ACCUM): the tile's rows go through a per-wave LDS transpose, then rows 2i and 2i+1 are added
-// to a per-wave LDS accumulator with one dim per lane (lanes 0-31 row 2i, 32-63 row 2i+1) by Kahan's
-// compensated sum; equal labels in a pair are added one after the other. Counts use LDS integer atomics
-// (exact, order-free); the inertia is a per-lane Kahan sum. The two waves' accumulators are folded in wave
-// order and written as the block's partial. Every accumulator has one writer and a fixed order of adds, so
-// the result is the same on every run.
+// Accumulation (ACCUM), also on the matrix cores: per 64-row block, sums (centres x dims) += onehot^T (centres x
+// rows) x rows. The one-hot operand is exact in bf16 (0 or 1); each row value is split exactly into three bf16
+// pieces (split3), so the float32 MFMA accumulators add the float32 row values themselves, rounded only by the
+// accumulation. Counts are integer-exact counts of the rows that did not match each centre; the inertia is a
+// per-lane Kahan sum. At the end of its rows each wave leaves its accumulators in LDS and the block folds them
+// in wave order (Neumaier across waves) into one partial per block; the partials are reduced in a fixed order
+// in float64 by a separate kernel. Every step has a fixed order, so the result is the same on every run.
 #pragma clang fp contract(off)
 #include "km_internal.h"
 #include <math.h>
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-#define KM_WAVES 2   // waves per block
 
 // ------------------------------------------------------------------ centre preparation
 
@@ -356,13 +355,12 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     float *Cl = lds;                                  // KP x CS float32 centres
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     char *wbase = reinterpret_cast<char *>(lds + KP * CS) + wave * WBYTES;
-    char *bufs[2] = {wbase, wbase + L::BUF};
     uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * L::BUF);   // labels of the block (0x4000: no row)
 
     const int64_t r_begin = (int64_t)blockIdx.x * rbs;
     const int64_t r_end = (r_begin + rbs < n) ? r_begin + rbs : n;
     int64_t r0 = r_begin + (int64_t)wave * 64;
-    if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, bufs[0]);
+    if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, wbase);
 
     for (int e = threadIdx.x; e < KP * CS; e += 64 * WAVES) {
         const int c = e / CS, j = e % CS;
@@ -394,13 +392,14 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     uint32_t rows_seen = 0;   // rows this lane compared
     const uint32_t ones = 0x00010001u, c3f80 = 0x3f803f80u, cneg = 0xc080c080u;
 
+    // the two block buffers alternate by offset (pointer arithmetic keeps the LDS address space visible)
     int cur = 0;
-    for (; r0 < r_end; r0 += 64 * WAVES, cur ^= 1) {
-        const char *buf = bufs[cur];
+    for (; r0 < r_end; r0 += 64 * WAVES, cur ^= L::BUF) {
+        const char *buf = wbase + cur;
         // ---- prefetch the next block into the other buffer, then wait for this one
         const int64_t r1 = r0 + 64 * WAVES;
         if (r1 < r_end) {
-            issue_block<D>(X, r1, r_end, lane, bufs[cur ^ 1]);
+            issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ L::BUF));
             if (L::QI == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
             else if (L::QI == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
             else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
