@@ -109,11 +109,12 @@ def main():
     ctx.set_parts([X])
     log(f"[bench] data on device: {n} x {d}, k={k}")
 
-    # warmup, then exactly `steps` Lloyd iterations timed by the host clock around device synchronisations
-    ctx.fit(C0, a.warmup, 0.0)
+    # warmup, then exactly `steps` Lloyd iterations timed by the host clock around device synchronisations.
+    # tol = -1 never stops the loop, so a workload that reaches a fixed point early still runs every pass.
+    ctx.fit(C0, a.warmup, -1.0)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    C, inertia, iters, _ = ctx.fit(C0, a.steps, 0.0)
+    C, inertia, iters, _ = ctx.fit(C0, a.steps, -1.0)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     assert iters == a.steps, (iters, a.steps)
@@ -122,7 +123,7 @@ def main():
 
     # dominant kernel: HIP events around every launch on the engine's stream, over the same loop
     ctx.profile(True)
-    ctx.fit(C0, a.steps, 0.0)
+    ctx.fit(C0, a.steps, -1.0)
     prof = ctx.profile_read()
     ctx.profile(False)
     kname, (kms, kcount) = max(prof.items(), key=lambda kv: kv[1][0])

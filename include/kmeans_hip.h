@@ -45,6 +45,8 @@ typedef struct km_ctx km_ctx;
 #define KM_PATH_AUTO 0
 #define KM_PATH_ROWS 1      /* direct-form scan of every centre on the vector ALUs (the reference's "rows") */
 #define KM_PATH_MFMA 2      /* bf16 matrix-core screen + exact rescoring of the candidates (the reference's "tiles") */
+#define KM_PATH_FUSED 3     /* dims <= 16: the rows loop fused with the accumulation, one read of the rows (the
+                             * reference's single-read "fused" / "onehot" kernels, core.py:1478-1534, 1562-1675) */
 
 /* Create a context on HIP device `device` (ordinal). NULL on failure (no context to carry a message).
  * Replaces the reference's module-global per-dataset caches (core.py:548-578): all state lives here. */
@@ -83,7 +85,7 @@ int32_t km_lloyd_step(km_ctx *ctx, const float *C, int32_t k, int32_t mode, int3
                       double *inertia, int32_t *n_empty);
 
 /* Up to max_iter Lloyd iterations from C0 (host, k x dims) with the reference's stopping rule
- * |prev - inertia| <= tol * prev (estimator.py:147-149), spherical renormalisation when spherical != 0
+ * |prev - inertia| <= tol * prev (estimator.py:147-149; a negative tol never stops a loop with inertia > 0), spherical renormalisation when spherical != 0
  * (estimator.py:127-130, 141-142). Iterations run back to back on the device; the host looks at the
  * device-side state only every few iterations and when a cluster empties. Outputs (host): C_out the final
  * centres, *last_inertia the inertia reported by the last iteration, *n_iter the iterations run,
@@ -98,7 +100,7 @@ int32_t km_profile(km_ctx *ctx, int32_t enable);
 int32_t km_profile_read(km_ctx *ctx, int32_t kernel, double *ms_total, int64_t *launches);
 const char *km_kernel_name(int32_t kernel);
 
-/* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS or KM_PATH_MFMA), and the number of
+/* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS, _MFMA or _FUSED), and the number of
  * rows in that pass that the MFMA screen could not settle alone: rows with more than one centre inside the
  * screen's error window, each rescored with the direct form against every centre in its window. */
 int32_t km_last_path(const km_ctx *ctx);

@@ -267,15 +267,25 @@ static int check_centres(km_ctx *c, const float *C, int32_t k) {
     return KM_OK;
 }
 
-// Decide the assignment path for this shape. MFMA when the screen serves the shape and pays; rows otherwise.
-static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
-    *mp = km_plan_mfma(c->n, c->d, k, 1);
+// Decide the assignment path for this shape: the matrix-core screen once a row's distance work is large
+// enough to hide its epilogue, the fused single-read scan for narrow rows, the generic two-kernel rows path
+// otherwise. An explicit path that does not serve the shape is an error (-1).
+static bool parts_aligned(const km_ctx *c) {
     for (auto &p : c->parts)
-        if (!p.aligned) mp->ok = 0;
+        if (!p.aligned) return false;
+    return true;
+}
+
+static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
+    const bool al = parts_aligned(c);
+    *mp = km_plan_mfma(c->n, c->d, k, 1);
+    if (!al) mp->ok = 0;
+    const bool lowd_ok = km_plan_lowd(c->n, c->d, k, al).ok != 0;
     if (path == KM_PATH_ROWS) return KM_PATH_ROWS;
     if (path == KM_PATH_MFMA) return mp->ok ? KM_PATH_MFMA : -1;
-    // auto: the screen pays once a row's distance work is large enough to hide its epilogue
+    if (path == KM_PATH_FUSED) return lowd_ok ? KM_PATH_FUSED : -1;
     if (mp->ok && c->d >= 16 && (int64_t)k * c->d >= 256) return KM_PATH_MFMA;
+    if (lowd_ok) return KM_PATH_FUSED;
     return KM_PATH_ROWS;
 }
 
@@ -311,7 +321,8 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
     km_mfma_plan mp;
     const int chosen = choose_path(c, k, path, &mp);
     if (chosen < 0)
-        return fail(c, KM_EINVAL, "path=mfma does not serve k=%d, dims=%d on this build", k, c->d);
+        return fail(c, KM_EINVAL, "path=%s does not serve k=%d, dims=%d on this build",
+                    path == KM_PATH_MFMA ? "mfma" : "fused", k, c->d);
     c->last_path = chosen;
     const int32_t *stop = gated ? &c->ctl->stop : nullptr;
     const int d = c->d;
@@ -341,6 +352,33 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
                 return km_launch_mfma(plans[i], 1, p.X, p.rows, d, c->C.p, k, aux, lab, bst, c->psum.p, c->pcomp.p,
                                       rb, c->ctl, stop, c->stream);
+            }));
+            rb += plans[i].nrb;
+            row0 += p.rows;
+        }
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->red.p, c->tot.p, stop, c->stream); }));
+        return KM_OK;
+    }
+
+    if (chosen == KM_PATH_FUSED) {
+        size_t total_rb = 0;
+        std::vector<km_lowd_plan> plans;
+        const bool al = parts_aligned(c);
+        for (auto &p : c->parts) {
+            plans.push_back(km_plan_lowd(p.rows, d, k, al));
+            total_rb += plans.back().nrb;
+        }
+        int r = ensure_pass_buffers(c, k, chosen, total_rb, false);
+        if (r) return r;
+        int rb = 0;
+        int64_t row0 = 0;
+        for (size_t i = 0; i < c->parts.size(); i++) {
+            const Part &p = c->parts[i];
+            uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
+            float *bst = best_d ? best_d + row0 : nullptr;
+            HIPCHK(c, launch(c, KK_FUSED_ROWS, [&] {
+                return km_launch_lowd(plans[i], p.X, p.rows, d, c->C.p, k, lab, bst, c->psum.p, c->pcomp.p, rb,
+                                      stop, c->stream);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;
@@ -579,7 +617,7 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     int r = check_centres(c, C0, k);
     if (r) return r;
     if (max_iter < 1) return fail(c, KM_EINVAL, "max_iter must be a positive integer");
-    if (!(tol >= 0.0) || !std::isfinite(tol)) return fail(c, KM_EINVAL, "tol must be finite and nonnegative");
+    if (std::isnan(tol)) return fail(c, KM_EINVAL, "tol must not be NaN");
     HIPCHK(c, hipSetDevice(c->device));
     if ((r = upload_centres(c, C0, k))) return r;
     if ((r = reset_control(c, tol))) return r;

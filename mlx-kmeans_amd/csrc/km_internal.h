@@ -90,3 +90,15 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused);
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int fused, const float *X, int64_t n, int d, const float *C,
                           int k, km_centre_aux aux, uint32_t *labels, float *best, float *psum, float *pcomp,
                           int rb0, km_control *ctl, const int32_t *stop, hipStream_t s);
+
+// Fused single-read pass for dims <= 16: exact rows loop + deterministic accumulation into per-block partials.
+struct km_lowd_plan {
+    int ok;          // 0 if the shape is not served (dims > 16, LDS too small, misaligned rows)
+    int64_t rbs;     // rows per block
+    int nrb;         // blocks
+    size_t lds;      // dynamic LDS bytes
+};
+km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned);
+hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int d, const float *C, int k,
+                          uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
+                          hipStream_t s);

@@ -14,8 +14,8 @@ LIB_PATH = os.path.join(_HERE, "libkmeans_hip.so")
 KM_OK, KM_EINVAL, KM_EDEVICE, KM_ENOMEM, KM_ENODATA = 0, -1, -2, -3, -4
 KM_HOST, KM_DEVICE = 0, 1
 KM_EXACT, KM_APPROX = 0, 1
-KM_PATH_AUTO, KM_PATH_ROWS, KM_PATH_MFMA = 0, 1, 2
-PATHS = {"auto": KM_PATH_AUTO, "rows": KM_PATH_ROWS, "mfma": KM_PATH_MFMA}
+KM_PATH_AUTO, KM_PATH_ROWS, KM_PATH_MFMA, KM_PATH_FUSED = 0, 1, 2, 3
+PATHS = {"auto": KM_PATH_AUTO, "rows": KM_PATH_ROWS, "mfma": KM_PATH_MFMA, "fused": KM_PATH_FUSED}
 
 # every symbol include/kmeans_hip.h declares: (name, restype, argtypes)
 _c = ctypes
@@ -173,7 +173,8 @@ class Context:
         return out
 
     def last_path(self):
-        return {KM_PATH_ROWS: "rows", KM_PATH_MFMA: "mfma"}.get(int(lib().km_last_path(self._h)), "none")
+        return {KM_PATH_ROWS: "rows", KM_PATH_MFMA: "mfma", KM_PATH_FUSED: "fused"}.get(
+            int(lib().km_last_path(self._h)), "none")
 
     def fallback_rows(self):
         return int(lib().km_last_fallback_rows(self._h))

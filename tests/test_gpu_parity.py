@@ -36,6 +36,14 @@ def mfma_served(d, k):
     return d in (16, 32) and k <= 64 or d == 64 and k <= 32
 
 
+def fused_served(d, k):
+    """The fused single-read path serves dims <= 16 with k * (dims + 2) <= 224 (its per-lane LDS tiles)."""
+    return d <= 16 and k * (d + 2) <= 224
+
+
+SERVED = {"rows": lambda d, k: True, "mfma": mfma_served, "fused": fused_served}
+
+
 def check_totals(tot, X, labels, best, ref_tot, scale):
     k = tot.shape[0]
     counts = np.rint(tot[:, 0]).astype(np.int64)
@@ -49,14 +57,14 @@ def check_totals(tot, X, labels, best, ref_tot, scale):
     assert k == ref_tot.shape[0]
 
 
-@pytest.mark.parametrize("path", ["rows", "mfma"])
+@pytest.mark.parametrize("path", ["rows", "mfma", "fused"])
 @pytest.mark.parametrize("name", G.CASES)
 def test_pass_matches_oracle(lib, name, path):
     fx = np.load(G.fixture_path(name))
     parts, C0, steps = G.case_inputs(name)
     d, k = C0.shape[1], C0.shape[0]
-    if path == "mfma" and not mfma_served(d, k):
-        pytest.skip(f"the fused mfma path serves d=16, 32 with k<=64 and d=64 with k<=32; not d={d} k={k}")
+    if not SERVED[path](d, k):
+        pytest.skip(f"path {path} does not serve d={d} k={k}")
     X = np.concatenate(parts)
     scale = float(np.sqrt((X.astype(np.float64) ** 2).mean())) or 1.0
     ctx = lib.Context()
@@ -122,27 +130,40 @@ def test_fit_loop_matches_oracle(lib, name):
     ctx.close()
 
 
-def test_paths_are_bit_identical(lib):
-    rng = np.random.default_rng(5)
-    for d, k in [(32, 64), (16, 64), (32, 32), (64, 32), (16, 32), (32, 40)]:
-        X = (rng.uniform(-3, 3, size=(k // 4, d))[rng.integers(0, k // 4, 60_000)]
-             + rng.standard_normal((60_000, d))).astype(np.float32)
-        C = X[rng.choice(len(X), k, replace=False)]
-        ctx = lib.Context()
-        ctx.set_parts([X])
-        say(f"[gpu] paths d={d} k={k}")
-        t1, l1, b1 = ctx.run_pass(C, path=lib.KM_PATH_ROWS, labels=True, best=True)
-        t2, l2, b2 = ctx.run_pass(C, path=lib.KM_PATH_MFMA, labels=True, best=True)
-        assert np.array_equal(l1, l2) and np.array_equal(b1.view(np.uint32), b2.view(np.uint32))
-        assert np.array_equal(np.rint(t1[:, 0]), np.rint(t2[:, 0]))
-        ctx.close()
+@pytest.mark.parametrize("d,k", [(32, 64), (16, 64), (32, 32), (64, 32), (16, 32), (32, 40), (16, 8), (12, 20),
+                                 (8, 8), (5, 33), (4, 12), (3, 7), (2, 64), (1, 5)])
+def test_paths_are_bit_identical(lib, d, k):
+    """Every path that serves a shape returns the rows path's labels and best bit for bit and the same counts;
+    sums agree to the accumulation tolerance. 60,011 rows: a ragged tail for every block size."""
+    rng = np.random.default_rng(5 + d * 1000 + k)
+    n = 60_011
+    X = (rng.uniform(-3, 3, size=(max(k // 4, 1), d))[rng.integers(0, max(k // 4, 1), n)]
+         + rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(len(X), k, replace=False)]
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] paths d={d} k={k}")
+    t1, l1, b1 = ctx.run_pass(C, path=lib.KM_PATH_ROWS, labels=True, best=True)
+    for name in ("mfma", "fused"):
+        if not SERVED[name](d, k):
+            continue
+        t2, l2, b2 = ctx.run_pass(C, path=lib.PATHS[name], labels=True, best=True)
+        assert ctx.last_path() == name
+        assert np.array_equal(l1, l2) and np.array_equal(b1.view(np.uint32), b2.view(np.uint32)), name
+        assert np.array_equal(np.rint(t1[:, 0]), np.rint(t2[:, 0])), name
+        cnt = np.maximum(np.rint(t1[:, 0]), 1)[:, None]
+        assert np.max(np.abs(t1[:, 2:] - t2[:, 2:]) / cnt) / scale <= CENTRE_TOL, name
+        np.testing.assert_allclose(t2[:, 1], t1[:, 1], rtol=1e-6, atol=1e-30)
+    ctx.close()
 
 
-def test_reruns_are_bit_identical(lib):
-    parts, C0, _ = G.case_inputs("outliers_d32")
+@pytest.mark.parametrize("name", ["outliers_d32", "lowd_d8", "pixels_d4"])
+def test_reruns_are_bit_identical(lib, name):
+    parts, C0, _ = G.case_inputs(name)
     ctx = lib.Context()
     ctx.set_parts(parts)
-    say("[gpu] reruns")
+    say(f"[gpu] reruns {name}")
     a = ctx.run_pass(C0, labels=True, best=True)
     b = ctx.run_pass(C0, labels=True, best=True)
     assert all(np.array_equal(x, y) for x, y in zip(a, b))
@@ -210,4 +231,36 @@ def test_headline_workload_full_size(lib):
     scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
     assert float(np.max(np.abs(C1.astype(np.float64) - C1_ref))) / scale <= CENTRE_TOL
     assert abs(inertia - inertia_ref) <= INERTIA_TOL * inertia_ref
+    ctx.close()
+
+
+@pytest.mark.parametrize("name", ["lowd_d8", "pixels_d4"])
+def test_lowd_workloads_full_size(lib, name):
+    """10M x 8, k=8 and 96M x 4, k=12 at full size on the fused single-read path: labels and best of a
+    200k-row sample bit-identical to the oracle's; counts sum to n; the per-cluster sums add up to the column
+    sums of X and the best sums to the oracle's inertia of the sample scaled check; a rerun gives the same bits."""
+    import oracle
+    from mlx_kmeans import synthetic
+    w = synthetic.WORKLOADS[name]()
+    X, C0, k = w["X"], w["C0"], w["k"]
+    n = len(X)
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] {name} full size n={n}")
+    tot, labels, best = ctx.run_pass(C0, labels=True, best=True)
+    assert ctx.last_path() == "fused"
+    rng = np.random.default_rng(2)
+    idx = np.sort(rng.choice(n, 200_000, replace=False))
+    ol, ob = oracle.assign(X[idx], C0)
+    assert np.array_equal(labels[idx], ol)
+    assert np.array_equal(best[idx].view(np.uint32), ob.view(np.uint32))
+    counts = np.rint(tot[:, 0]).astype(np.int64)
+    assert int(counts.sum()) == n
+    assert np.array_equal(counts, np.bincount(labels, minlength=k))
+    colsum = X.astype(np.float64).sum(0)
+    assert np.max(np.abs(tot[:, 2:].sum(0) - colsum)) <= 1e-6 * np.abs(X).astype(np.float64).sum(0).max()
+    bsum = np.bincount(labels, weights=best.astype(np.float64), minlength=k)
+    np.testing.assert_allclose(tot[:, 1], bsum, rtol=1e-6)
+    tot2, labels2, _ = ctx.run_pass(C0, labels=True)
+    assert np.array_equal(tot, tot2) and np.array_equal(labels, labels2)
     ctx.close()
