@@ -1,14 +1,15 @@
 // libkmeans_hip.so: the C ABI (include/kmeans_hip.h) and the host runtime around the kernels.
 //
-// A context owns one HIP stream, the device copies (or borrowed pointers) of the data slices, the current
-// centres, and every workspace of a pass. A Lloyd iteration is a fixed sequence of kernels on that stream:
-//   prep (centre norms, bf16 operand)  ->  assignment + accumulation into per-block partials
-//   ->  reduce to float64 totals  ->  update stats (counts, inertia, empties, stopping rule)
-//   ->  update centres (in place)  [-> spherical renormalisation]
-// The update kernels keep the loop state in a device-side km_control block, and every kernel of a pass is
-// gated on it, so km_fit queues iterations back to back and looks at the state only every KM_FIT_BATCH
-// iterations. A pass that leaves clusters empty stops the queue; the host then relocates them the way the
-// reference's lloyd_step does (core.py:2222-2242) and resumes.
+// A context owns one HIP stream, the device copies (or borrowed pointers) of the data slices, two centre buffers,
+// and every workspace of a pass. A Lloyd iteration is three kernels on that stream:
+//   assignment + accumulation into per-block partials (fused MFMA, fused rows, or the generic pair)
+//   ->  k_reduce_split (float64 sums of fixed ranges of partials)
+//   ->  k_finish (totals; new centres into the other buffer; in its last block the statistics and stopping rule)
+// Pass p reads centre buffer p % 2 and writes buffer (p + 1) % 2. The loop state lives in a device-side
+// km_control block and every kernel of a pass is gated on it, so km_fit queues iterations back to back and looks
+// at the state only every KM_FIT_BATCH iterations. A pass that leaves clusters empty stops the queue; the host
+// then relocates them the way the reference's lloyd_step does (core.py:2222-2242), from that pass's input
+// centres and totals, and resumes.
 #include "kmeans_hip.h"
 #include "km_internal.h"
 
@@ -65,13 +66,11 @@ struct km_ctx {
     int64_t n = 0;
     std::string err;
     int32_t last_path = 0;
-    DBuf<float> C;          // current centres (k, d)
-    DBuf<float> csq, cnorm, maxes;
-    DBuf<uint16_t> cb;
+    DBuf<float> Cb[2];      // centre buffers (k, d): pass p reads Cb[p & 1], writes Cb[(p + 1) & 1]
     DBuf<float> psum, pcomp;
     DBuf<double> tot;
     DBuf<double> tot2;      // (k, 2) [count, best] totals recomputed for km_pass on the fused path
-    DBuf<double> red;       // stage-1 sums of the reduce
+    DBuf<double> red;       // range sums of the reduce (S, k * (d + 2))
     DBuf<uint32_t> labels;
     DBuf<float> best;
     km_control *ctl = nullptr;    // device
@@ -176,11 +175,8 @@ extern "C" void km_destroy(km_ctx *c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     drop_parts(c);
-    c->C.release();
-    c->csq.release();
-    c->cnorm.release();
-    c->maxes.release();
-    c->cb.release();
+    c->Cb[0].release();
+    c->Cb[1].release();
     c->psum.release();
     c->pcomp.release();
     c->tot.release();
@@ -295,7 +291,7 @@ static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bo
     HIPCHK(c, c->psum.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->tot.ensure((size_t)kw));
-    HIPCHK(c, c->red.ensure(km_reduce_tmp_doubles((int)total_rb, kw)));
+    HIPCHK(c, c->red.ensure((size_t)km_reduce_splits((int)total_rb, kw) * kw));
     if (need_rows_scratch) {
         HIPCHK(c, c->labels.ensure((size_t)c->n));
         HIPCHK(c, c->best.ensure((size_t)c->n));
@@ -304,20 +300,26 @@ static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bo
     return KM_OK;
 }
 
-static km_centre_aux aux_of(km_ctx *c) {
-    km_centre_aux a;
-    a.csq = c->csq.p;
-    a.cnorm = c->cnorm.p;
-    a.maxes = c->maxes.p;
-    a.cb = c->cb.p;
-    return a;
+// Partials -> totals in c->tot, and with KM_FIN_UPDATE the new centres into Cb[(pass + 1) & 1] and the pass
+// statistics into the control block.
+static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags, const int32_t *stop) {
+    const int d = c->d;
+    const int64_t kw = (int64_t)k * (d + 2);
+    const int S = km_reduce_splits(rb, kw);
+    HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce_split(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, stop, c->stream); }));
+    float *Cn = c->Cb[(pass + 1) & 1].p;
+    HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, S, k, d, c->tot.p, Cn, c->ctl, pass, tol, flags, stop, c->stream); }));
+    return KM_OK;
 }
 
-// One assignment + accumulation pass over every slice with the centres in c->C, leaving float64 totals in
-// c->tot. labels_d/best_d: device arrays of n (or null) to receive the per-row results. gated: every kernel
-// checks ctl->stop.
-static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, float *best_d, bool gated) {
+// Pass `pass`: assignment + accumulation over every slice with the centres in Cb[pass & 1], then the finish
+// (float64 totals in c->tot; with KM_FIN_UPDATE in flags the new centres and the statistics). labels_d/best_d:
+// device arrays of n (or null) for the per-row results. gated: every kernel checks ctl->stop first.
+static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, float *best_d, bool gated, int pass,
+                    double tol, int flags) {
     (void)mode;
+    HIPCHK(c, c->Cb[(pass + 1) & 1].ensure((size_t)k * c->d));
+    const float *Cin = c->Cb[pass & 1].p;
     km_mfma_plan mp;
     const int chosen = choose_path(c, k, path, &mp);
     if (chosen < 0)
@@ -337,12 +339,6 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         }
         int r = ensure_pass_buffers(c, k, chosen, total_rb, false);
         if (r) return r;
-        HIPCHK(c, c->csq.ensure(mp.kpad));
-        HIPCHK(c, c->cnorm.ensure(mp.kpad));
-        HIPCHK(c, c->maxes.ensure(4));
-        HIPCHK(c, c->cb.ensure((size_t)mp.kpad * (mp.dpad + 16)));
-        km_centre_aux aux = aux_of(c);
-        HIPCHK(c, launch(c, KK_PREP, [&] { return km_launch_prep(c->C.p, k, d, mp.kpad, mp.dpad, aux, stop, c->stream); }));
         int rb = 0;
         int64_t row0 = 0;
         for (size_t i = 0; i < c->parts.size(); i++) {
@@ -350,14 +346,13 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
             float *bst = best_d ? best_d + row0 : nullptr;
             HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
-                return km_launch_mfma(plans[i], 1, p.X, p.rows, d, c->C.p, k, aux, lab, bst, c->psum.p, c->pcomp.p,
-                                      rb, c->ctl, stop, c->stream);
+                return km_launch_mfma(plans[i], 1, p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p, rb,
+                                      c->ctl, stop, c->stream);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->red.p, c->tot.p, stop, c->stream); }));
-        return KM_OK;
+        return finish_pass(c, k, rb, pass, tol, flags, stop);
     }
 
     if (chosen == KM_PATH_FUSED) {
@@ -377,14 +372,13 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
             float *bst = best_d ? best_d + row0 : nullptr;
             HIPCHK(c, launch(c, KK_FUSED_ROWS, [&] {
-                return km_launch_lowd(plans[i], p.X, p.rows, d, c->C.p, k, lab, bst, c->psum.p, c->pcomp.p, rb,
-                                      stop, c->stream);
+                return km_launch_lowd(plans[i], p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p, rb, stop,
+                                      c->stream);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->red.p, c->tot.p, stop, c->stream); }));
-        return KM_OK;
+        return finish_pass(c, k, rb, pass, tol, flags, stop);
     }
 
     // rows path: exact labels for every slice, then the generic accumulation
@@ -403,7 +397,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
     for (size_t i = 0; i < c->parts.size(); i++) {
         const Part &p = c->parts[i];
         HIPCHK(c, launch(c, KK_ASSIGN_ROWS, [&] {
-            return km_launch_assign_rows(p.X, p.rows, d, c->C.p, k, lab_all + row0, best_all + row0, stop, c->stream);
+            return km_launch_assign_rows(p.X, p.rows, d, Cin, k, lab_all + row0, best_all + row0, stop, c->stream);
         }));
         HIPCHK(c, launch(c, KK_ACCUM_GENERIC, [&] {
             return km_launch_accum_generic(plans[i], p.X, p.rows, d, lab_all + row0, best_all + row0, k, c->psum.p,
@@ -412,21 +406,21 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         rb += plans[i].nrb;
         row0 += p.rows;
     }
-    HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, kw, c->red.p, c->tot.p, stop, c->stream); }));
-    return KM_OK;
+    return finish_pass(c, k, rb, pass, tol, flags, stop);
 }
 
-// Labels and best for every row with the centres in c->C, into c->labels / c->best (no accumulation needed by
-// the caller, but the pass runs in full: it is the same code as every other pass, so the same bits).
-static int run_labels(km_ctx *c, int k, int mode, int path) {
+// Labels and best for every row with the centres in Cb[pass & 1], into c->labels / c->best. The pass runs in
+// full (it is the same code as every other pass, so the same bits) but updates nothing.
+static int run_labels(km_ctx *c, int k, int mode, int path, int pass) {
     HIPCHK(c, c->labels.ensure((size_t)c->n));
     HIPCHK(c, c->best.ensure((size_t)c->n));
-    return run_pass(c, k, mode, path, c->labels.p, c->best.p, false);
+    return run_pass(c, k, mode, path, c->labels.p, c->best.p, false, pass, 0.0, 0);
 }
 
 static int upload_centres(km_ctx *c, const float *C, int k) {
-    HIPCHK(c, c->C.ensure((size_t)k * c->d));
-    HIPCHK(c, hipMemcpyAsync(c->C.p, C, (size_t)k * c->d * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, c->Cb[0].ensure((size_t)k * c->d));
+    HIPCHK(c, c->Cb[1].ensure((size_t)k * c->d));
+    HIPCHK(c, hipMemcpyAsync(c->Cb[0].p, C, (size_t)k * c->d * sizeof(float), hipMemcpyHostToDevice, c->stream));
     return KM_OK;
 }
 
@@ -462,7 +456,7 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
     HIPCHK(c, c->labels.ensure((size_t)c->n));
     HIPCHK(c, c->best.ensure((size_t)c->n));
     if ((r = reset_control(c, 0.0))) return r;
-    if ((r = run_pass(c, k, mode, path, c->labels.p, c->best.p, false))) return r;
+    if ((r = run_pass(c, k, mode, path, c->labels.p, c->best.p, false, 0, 0.0, 0))) return r;
     const int w = c->d + 2;
     const int64_t kw = (int64_t)k * w;
     HIPCHK(c, hipMemcpyAsync(totals, c->tot.p, kw * sizeof(double), hipMemcpyDeviceToHost, c->stream));
@@ -480,7 +474,8 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
         HIPCHK(c, c->psum.ensure(total_rb * (size_t)k * 2));
         HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)k * 2));
         HIPCHK(c, c->tot2.ensure((size_t)k * 2));
-        HIPCHK(c, c->red.ensure(km_reduce_tmp_doubles((int)total_rb, (int64_t)k * 2)));
+        const int S2 = km_reduce_splits((int)total_rb, (int64_t)k * 2);
+        HIPCHK(c, c->red.ensure((size_t)S2 * k * 2));
         int rb = 0;
         int64_t row0 = 0;
         for (size_t i = 0; i < c->parts.size(); i++) {
@@ -492,7 +487,8 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, c->red.p, c->tot2.p, nullptr, c->stream); }));
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce_split(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, S2, c->red.p, nullptr, c->stream); }));
+        HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, S2, k, 0, c->tot2.p, nullptr, c->ctl, 0, 0.0, 0, nullptr, c->stream); }));
         cb2.resize((size_t)k * 2);
         HIPCHK(c, hipMemcpyAsync(cb2.data(), c->tot2.p, cb2.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
     }
@@ -507,11 +503,12 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
 
 // ------------------------------------------------------------------ relocation of empty clusters (host side)
 //
-// The pass whose stats kernel flagged empties left its totals in c->tot and its input centres in c->C.
+// The pass `pass` whose statistics flagged empties left its totals in c->tot and its input centres in
+// Cb[pass & 1]; the relocated centres go to Cb[(pass + 1) & 1].
 // Following lloyd_step (core.py:2222-2242): the empty clusters, in ascending order, take the rows with the
 // largest best distance (ties: lower row index); each such row leaves its old cluster; centres are the
 // float64 means rounded to float32; a cluster still empty takes the largest cluster's centre.
-static int relocate(km_ctx *c, int k, int mode, int path, int *n_empty_out) {
+static int relocate(km_ctx *c, int k, int mode, int path, int pass, int *n_empty_out) {
     const int d = c->d, w = d + 2;
     std::vector<double> tot((size_t)k * w);
     HIPCHK(c, hipMemcpyAsync(tot.data(), c->tot.p, tot.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
@@ -526,7 +523,7 @@ static int relocate(km_ctx *c, int k, int mode, int path, int *n_empty_out) {
     }
     *n_empty_out = (int)empty.size();
     if (!empty.empty()) {
-        int r = run_labels(c, k, mode, path);
+        int r = run_labels(c, k, mode, path, pass);
         if (r) return r;
         std::vector<float> best(c->n);
         std::vector<uint32_t> labels(c->n);
@@ -570,21 +567,16 @@ static int relocate(km_ctx *c, int k, int mode, int path, int *n_empty_out) {
     for (int j = 0; j < k; j++)
         if (counts[j] <= 0)
             for (int e = 0; e < d; e++) Cn[(size_t)j * d + e] = Cn[(size_t)big * d + e];
-    HIPCHK(c, hipMemcpyAsync(c->C.p, Cn.data(), Cn.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->Cb[(pass + 1) & 1].p, Cn.data(), Cn.size() * sizeof(float), hipMemcpyHostToDevice,
+                             c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return KM_OK;
 }
 
-// Queues pass `pass` of a loop: the pass itself, then the update stage.
+// Queues pass `pass` of a loop, gated on the control block.
 static int queue_iteration(km_ctx *c, int k, int mode, int path, int pass, double tol, int spherical) {
-    int r = run_pass(c, k, mode, path, nullptr, nullptr, true);
-    if (r) return r;
-    const int d = c->d;
-    HIPCHK(c, launch(c, KK_UPDATE_STATS, [&] { return km_launch_update_stats(c->tot.p, k, d + 2, c->ctl, pass, tol, c->stream); }));
-    HIPCHK(c, launch(c, KK_UPDATE_CENTRES, [&] { return km_launch_update_centres(c->tot.p, k, d, c->ctl, pass, c->C.p, c->stream); }));
-    if (spherical)
-        HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->C.p, k, d, c->ctl, pass, c->stream); }));
-    return KM_OK;
+    return run_pass(c, k, mode, path, nullptr, nullptr, true, pass, tol,
+                    KM_FIN_UPDATE | (spherical ? KM_FIN_SPHERICAL : 0));
 }
 
 extern "C" int32_t km_lloyd_step(km_ctx *c, const float *C, int32_t k, int32_t mode, int32_t path, float *C_out,
@@ -600,9 +592,9 @@ extern "C" int32_t km_lloyd_step(km_ctx *c, const float *C, int32_t k, int32_t m
     if ((r = read_control(c))) return r;
     int ne = c->ctl_h->n_empty;
     if (c->ctl_h->need_reloc) {
-        if ((r = relocate(c, k, mode, path, &ne))) return r;
+        if ((r = relocate(c, k, mode, path, 0, &ne))) return r;
     }
-    HIPCHK(c, hipMemcpyAsync(C_out, c->C.p, (size_t)k * c->d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(C_out, c->Cb[1].p, (size_t)k * c->d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if (inertia) *inertia = c->ctl_h->inertia;
     if (n_empty) *n_empty = ne;
@@ -621,7 +613,7 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     HIPCHK(c, hipSetDevice(c->device));
     if ((r = upload_centres(c, C0, k))) return r;
     if ((r = reset_control(c, tol))) return r;
-    if (spherical) HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->C.p, k, c->d, c->ctl, -1, c->stream); }));
+    if (spherical) HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->Cb[0].p, k, c->d, c->stream); }));
     const int path = KM_PATH_AUTO;
     int pass = 0, relocated = 0;
     while (pass < max_iter) {
@@ -632,16 +624,20 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
         pass = c->ctl_h->iter;
         if (c->ctl_h->need_reloc) {
             int ne = 0;
-            if ((r = relocate(c, k, mode, path, &ne))) return r;
+            const int q = c->ctl_h->iter - 1;   // the pass that left clusters empty
+            if ((r = relocate(c, k, mode, path, q, &ne))) return r;
             relocated += ne;
-            if (spherical) HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->C.p, k, c->d, c->ctl, -1, c->stream); }));
+            if (spherical)
+                HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->Cb[(q + 1) & 1].p, k, c->d, c->stream); }));
             c->ctl_h->need_reloc = 0;
             c->ctl_h->stop = c->ctl_h->done;
             if ((r = write_control(c))) return r;
         }
         if (c->ctl_h->done) break;
     }
-    if (C_out) HIPCHK(c, hipMemcpyAsync(C_out, c->C.p, (size_t)k * c->d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    if (C_out)
+        HIPCHK(c, hipMemcpyAsync(C_out, c->Cb[c->ctl_h->iter & 1].p, (size_t)k * c->d * sizeof(float),
+                                 hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if (last_inertia) *last_inertia = c->ctl_h->inertia;
     if (n_iter) *n_iter = c->ctl_h->iter;

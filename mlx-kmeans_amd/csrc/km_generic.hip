@@ -5,19 +5,19 @@
 //                     (reference: mlx_kmeans/core.py:263-274, the rows loop)
 //   k_accum_generic   deterministic compensated per-cluster [count, best, x] into per-row-block partials
 //                     (reference: the accumulation paths of core.py:1292-1466; Neumaier add of core.py:244-247)
-//   k_reduce          partials -> float64 totals in row-block order
-//   k_update_stats    counts, inertia, empties, argmax, stopping rule (core.py:2222-2242, estimator.py:147-149)
-//   k_update_centres  centres = sums / counts in float64, rounded to float32 (core.py:2238-2242)
-//   k_normalise       spherical renormalisation (estimator.py:127-130)
+//   k_reduce_split    partials -> float64 sums of fixed contiguous ranges of row-blocks
+//   k_finish          totals, new centres (core.py:2238-2242), spherical renormalisation (estimator.py:127-130),
+//                     and in its last block the counts, inertia, empties, argmax and stopping rule
+//                     (core.py:2222-2242, estimator.py:147-149)
+//   k_normalise       spherical renormalisation of host-given centres (the start of a fit, after a relocation)
 //
 // The file is compiled with -ffp-contract=off: `s + t * t` stays a separately rounded product and add.
 #pragma clang fp contract(off)
 #include "km_internal.h"
 #include <math.h>
 
-const char *const km_kernel_names[KK_COUNT] = {
-    "km_prep", "km_assign_rows", "km_accum_generic", "km_reduce", "km_update_stats",
-    "km_update_centres", "km_normalise", "km_fused_rows", "km_fused_mfma", "km_assign_mfma"};
+const char *const km_kernel_names[KK_COUNT] = {"km_assign_rows", "km_accum_generic", "km_reduce", "km_finish",
+                                                "km_normalise",   "km_fused_rows",    "km_fused_mfma"};
 
 // Neumaier's compensated add, the reference's KAHAN_ADD (core.py:244-247): t = s + v; the rounding error of
 // that add goes to c; the true running sum is s + c.
@@ -209,81 +209,88 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
     return hipGetLastError();
 }
 
-// ------------------------------------------------------------------ partials -> float64 totals
+// ------------------------------------------------------------------ partials -> totals -> update
 //
-// Two stages, both in fixed order: stage 1 splits the row-blocks into KM_RED_SPLIT contiguous ranges and sums
-// each range per slot in float64; stage 2 adds the ranges in order. The partition depends only on the number of
-// row-blocks, so the result is the same on every run.
+// Two or three kernels finish a pass, all in a fixed order, none communicating across blocks. k_reduce_split
+// cuts the row-block partials into S contiguous ranges (S depends only on the number of row-blocks and the
+// entry count) and sums each range per entry in float64: sixteen waves take sixteen fixed sub-ranges and add
+// their sums in wave order. The finish adds the S range sums in order into the float64 totals (columns
+// [count, best, x...]) and, when the pass updates, writes the new centres float(sum / count)
+// (core.py:2238-2242) into the other centre buffer, renormalised for spherical k-means (estimator.py:127-130),
+// then the pass statistics in a fixed order - counts, inertia, empty clusters, the largest cluster - and the
+// stopping rule (core.py:2222-2242, estimator.py:147-149); clusters that stayed empty with no row to take get
+// the largest cluster's centre. Up to KM_FIN1_MAX entries one 1024-thread block does all of it (k_finish1);
+// beyond, one block per cluster (k_finish) and one block for the statistics (k_stats).
 
-static constexpr int KM_RED_SPLIT = 64;
+static constexpr int KM_FIN1_MAX = 4096;   // entries k * (d + 2) finished by a single block (LDS)
+static constexpr int KM_FIN1_SPLITS = 16;  // range sums read per entry by the single block
 
-__global__ __launch_bounds__(256) void k_reduce1(const float *__restrict__ psum, const float *__restrict__ pcomp,
-                                                 int nrb, int64_t kw, int split, double *__restrict__ tmp,
-                                                 const int32_t *__restrict__ stop) {
+int km_reduce_splits(int nrb, int64_t kw) {
+    const int cap = kw <= KM_FIN1_MAX ? KM_FIN1_SPLITS : 64;
+    int s = nrb / 16;
+    if (s > cap) s = cap;
+    if (s < 1) s = 1;
+    return s;
+}
+
+__global__ __launch_bounds__(1024) void k_reduce_split(const float *__restrict__ psum,
+                                                       const float *__restrict__ pcomp, int nrb, int64_t kw, int S,
+                                                       double *__restrict__ tmp, const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= kw) return;
-    const int s = blockIdx.y;
-    const int r0 = (int)((int64_t)nrb * s / split), r1 = (int)((int64_t)nrb * (s + 1) / split);
+    __shared__ double part[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int sp = blockIdx.y;
+    const int r0 = (int)((int64_t)nrb * sp / S), r1 = (int)((int64_t)nrb * (sp + 1) / S);
+    const int len = r1 - r0;
+    const int q0 = r0 + (int)((int64_t)len * wave / 16), q1 = r0 + (int)((int64_t)len * (wave + 1) / 16);
     double acc = 0.0;
-    for (int r = r0; r < r1; r++) acc += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
-    tmp[(int64_t)s * kw + e] = acc;
+    if (e < kw) {
+#pragma unroll 4
+        for (int r = q0; r < q1; r++) acc += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && e < kw) {
+        double t = part[0][lane];
+        for (int w = 1; w < 16; w++) t += part[w][lane];
+        tmp[(int64_t)sp * kw + e] = t;
+    }
 }
 
-__global__ __launch_bounds__(256) void k_reduce2(const double *__restrict__ tmp, int64_t kw, int split,
-                                                 double *__restrict__ tot, const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= kw) return;
-    double acc = 0.0;
-    for (int s = 0; s < split; s++) acc += tmp[(int64_t)s * kw + e];
-    tot[e] = acc;
-}
-
-size_t km_reduce_tmp_doubles(int nrb, int64_t kw) {
-    const int split = nrb < KM_RED_SPLIT ? nrb : KM_RED_SPLIT;
-    return (size_t)split * kw;
-}
-
-hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tmp, double *tot,
-                            const int32_t *stop, hipStream_t s) {
-    const int split = nrb < KM_RED_SPLIT ? (nrb < 1 ? 1 : nrb) : KM_RED_SPLIT;
-    const unsigned gx = (unsigned)((kw + 255) / 256);
-    hipLaunchKernelGGL(k_reduce1, dim3(gx, split), dim3(256), 0, s, psum, pcomp, nrb, kw, split, tmp, stop);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_reduce2, dim3(gx), dim3(256), 0, s, tmp, kw, split, tot, stop);
+hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
+                                  const int32_t *stop, hipStream_t s) {
+    hipLaunchKernelGGL(k_reduce_split, dim3((unsigned)((kw + 63) / 64), S), dim3(1024), 0, s, psum, pcomp, nrb, kw,
+                       S, tmp, stop);
     return hipGetLastError();
 }
 
-// ------------------------------------------------------------------ update stage
-
-// One block of 256 threads. Counts are rint(tot[c, 0]) (exact integers in every partial). The inertia is the
-// sum of tot[:, 1] in a fixed order (per-thread strided sums, then a fixed tree), so it is reproducible.
-__global__ __launch_bounds__(256) void k_update_stats(const double *__restrict__ tot, int k, int w,
-                                                      km_control *__restrict__ ctl, int pass, double tol) {
-    if (ctl->stop) return;
-    __shared__ double s_in[256];
-    __shared__ int s_empty[256];
-    __shared__ long long s_max[256];
-    __shared__ int s_arg[256];
-    const int tid = threadIdx.x;
+// The pass statistics from the totals (counts in column 0, best sums in column 1), by `nthreads` threads of
+// one block: strided per-thread sums over clusters ascending, then a fixed tree. Writes the control block and
+// gives still-empty clusters (when no relocation is due) the largest cluster's centre.
+template <int NT>
+__device__ void pass_stats(const double *tot, int k, int d, float *Cnext, km_control *ctl, int pass, double tol) {
+    const int tid = threadIdx.x, W = d + 2;
+    __shared__ double s_in[NT];
+    __shared__ int s_empty[NT];
+    __shared__ long long s_max[NT];
+    __shared__ int s_arg[NT];
     double in = 0.0;
     int empty = 0;
     long long mx = -1;
     int arg = 0;
-    for (int c = tid; c < k; c += 256) {
-        const long long cnt = llrint(tot[(size_t)c * w]);
-        in += tot[(size_t)c * w + 1];
-        empty += cnt == 0;
-        if (cnt > mx) { mx = cnt; arg = c; }   // strided ascending c: first maximum within this thread
+    for (int cc = tid; cc < k; cc += NT) {
+        const long long n_c = llrint(tot[(int64_t)cc * W]);
+        in += tot[(int64_t)cc * W + 1];
+        empty += n_c == 0;
+        if (n_c > mx) { mx = n_c; arg = cc; }   // strided ascending cc: the first maximum within this thread
     }
     s_in[tid] = in;
     s_empty[tid] = empty;
     s_max[tid] = mx;
     s_arg[tid] = arg;
     __syncthreads();
-    for (int h = 128; h > 0; h >>= 1) {
+    for (int h = NT / 2; h > 0; h >>= 1) {
         if (tid < h) {
             s_in[tid] += s_in[tid + h];
             s_empty[tid] += s_empty[tid + h];
@@ -293,61 +300,137 @@ __global__ __launch_bounds__(256) void k_update_stats(const double *__restrict__
         }
         __syncthreads();
     }
+    const double inertia = s_in[0];
+    const int ne = s_empty[0], big = s_arg[0];
+    const int need_reloc = (ne > 0 && inertia > 0.0) ? 1 : 0;
     if (tid == 0) {
-        const double inertia = s_in[0];
-        const int ne = s_empty[0];
         int done = 0;
         if (pass > 0 && fabs(ctl->prev - inertia) <= tol * ctl->prev) done = 1;
         ctl->prev = inertia;
         ctl->inertia = inertia;
         ctl->n_empty = ne;
-        ctl->big = s_arg[0];
-        ctl->need_reloc = (ne > 0 && inertia > 0.0) ? 1 : 0;
+        ctl->big = big;
+        ctl->need_reloc = need_reloc;
         ctl->done = done;
         ctl->iter = pass + 1;
-        ctl->stop = (done || ctl->need_reloc) ? 1 : 0;
+        ctl->stop = (done || need_reloc) ? 1 : 0;
+    }
+    if (ne > 0 && !need_reloc) {
+        for (int cc = 0; cc < k; cc++) {
+            if (llrint(tot[(int64_t)cc * W]) != 0) continue;
+            for (int j = tid; j < d; j += NT) Cnext[(int64_t)cc * d + j] = Cnext[(int64_t)big * d + j];
+        }
     }
 }
 
-hipError_t km_launch_update_stats(const double *tot, int k, int w, km_control *ctl, int pass, double tol,
-                                  hipStream_t s) {
-    hipLaunchKernelGGL(k_update_stats, dim3(1), dim3(256), 0, s, tot, k, w, ctl, pass, tol);
-    return hipGetLastError();
+// Renormalise centre c of Cnext with one wave (lanes over dims, float64 sum, fixed butterfly).
+__device__ void normalise_row(float *Cnext, int c, int d, int lane) {
+    float *row = Cnext + (int64_t)c * d;
+    double sq = 0.0;
+    for (int j = lane; j < d; j += 64) sq += (double)row[j] * (double)row[j];
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    const float nrm = (float)sqrt(sq);
+    if (nrm > 0.0f)
+        for (int j = lane; j < d; j += 64) row[j] = row[j] / nrm;
 }
 
-// C[c, j] = float(sum / count). Runs only for the pass whose stats just completed (ctl->iter == pass + 1)
-// and only when no relocation is pending (the host performs that update). A cluster still empty here can
-// only be one with no rows to give it (every best was 0): it takes the largest cluster's centre.
-__global__ __launch_bounds__(256) void k_update_centres(const double *__restrict__ tot, int k, int d,
-                                                        const km_control *__restrict__ ctl, int pass,
-                                                        float *__restrict__ C) {
-    if (ctl->iter != pass + 1 || ctl->need_reloc) return;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= (int64_t)k * d) return;
-    const int w = d + 2;
-    int c = (int)(e / d);
-    const int j = (int)(e % d);
-    long long cnt = llrint(tot[(size_t)c * w]);
-    if (cnt <= 0) {
-        c = ctl->big;
-        cnt = llrint(tot[(size_t)c * w]);
+__global__ __launch_bounds__(1024) void k_finish1(const double *__restrict__ tmp, int S, int k, int d,
+                                                  double *__restrict__ tot, float *__restrict__ Cnext,
+                                                  km_control *__restrict__ ctl, int pass, double tol, int flags,
+                                                  const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ double Ts[];   // the totals, k * (d + 2)
+    const int tid = threadIdx.x, W = d + 2;
+    const int kw = k * W;
+    for (int e = tid; e < kw; e += 1024) {
+        double v[KM_FIN1_SPLITS];
+#pragma unroll
+        for (int sp = 0; sp < KM_FIN1_SPLITS; sp++) v[sp] = sp < S ? tmp[(int64_t)sp * kw + e] : 0.0;
+        double t = v[0];
+#pragma unroll
+        for (int sp = 1; sp < KM_FIN1_SPLITS; sp++)
+            if (sp < S) t += v[sp];
+        Ts[e] = t;
+        tot[e] = t;
     }
-    C[e] = (float)(tot[(size_t)c * w + 2 + j] / (double)cnt);
+    __syncthreads();
+    if (!(flags & KM_FIN_UPDATE)) return;
+    for (int e = tid; e < k * d; e += 1024) {
+        const int c = e / d, j = e - (e / d) * d;
+        const long long cnt = llrint(Ts[c * W]);
+        if (cnt > 0) Cnext[e] = (float)(Ts[c * W + 2 + j] / (double)cnt);
+    }
+    __syncthreads();
+    if (flags & KM_FIN_SPHERICAL) {
+        const int wave = tid >> 6, lane = tid & 63;
+        for (int c = wave; c < k; c += 16)
+            if (llrint(Ts[c * W]) > 0) normalise_row(Cnext, c, d, lane);
+        __syncthreads();
+    }
+    pass_stats<1024>(Ts, k, d, Cnext, ctl, pass, tol);
 }
 
-hipError_t km_launch_update_centres(const double *tot, int k, int d, km_control *ctl, int pass, float *C,
-                                    hipStream_t s) {
-    const int64_t kd = (int64_t)k * d;
-    hipLaunchKernelGGL(k_update_centres, dim3((unsigned)((kd + 255) / 256)), dim3(256), 0, s, tot, k, d, ctl,
-                       pass, C);
+__global__ __launch_bounds__(256) void k_finish(const double *__restrict__ tmp, int S, int k, int d,
+                                                double *__restrict__ tot, float *__restrict__ Cnext, int flags,
+                                                const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int c = blockIdx.x, tid = threadIdx.x, W = d + 2;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int64_t kw = (int64_t)k * W;
+    __shared__ double s_cnt;
+    // entry j of this cluster = the sum of its S range sums, lane s taking range s (S <= 64) and a fixed
+    // butterfly adding them; wave w takes entries w, w + 4, ...; the count (entry 0) first
+    const double *src = tmp + (int64_t)c * W;
+    if (wave == 0) {
+        double v = lane < S ? src[(int64_t)lane * kw] : 0.0;
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) {
+            tot[(int64_t)c * W] = v;
+            s_cnt = v;
+        }
+    }
+    __syncthreads();
+    const long long cnt = llrint(s_cnt);
+    const bool update = (flags & KM_FIN_UPDATE) != 0;
+    for (int j = 1 + wave; j < W; j += 4) {
+        double v = lane < S ? src[(int64_t)lane * kw + j] : 0.0;
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) {
+            tot[(int64_t)c * W + j] = v;
+            if (update && j >= 2 && cnt > 0) Cnext[(int64_t)c * d + (j - 2)] = (float)(v / (double)cnt);
+        }
+    }
+    if (update && (flags & KM_FIN_SPHERICAL) && cnt > 0) {
+        __syncthreads();
+        if (wave == 0) normalise_row(Cnext, c, d, lane);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_stats(const double *__restrict__ tot, int k, int d,
+                                               float *__restrict__ Cnext, km_control *__restrict__ ctl, int pass,
+                                               double tol, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    pass_stats<256>(tot, k, d, Cnext, ctl, pass, tol);
+}
+
+hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,
+                            int pass, double tol, int flags, const int32_t *stop, hipStream_t s) {
+    const int64_t kw = (int64_t)k * (d + 2);
+    if (kw <= KM_FIN1_MAX && S <= KM_FIN1_SPLITS) {
+        hipLaunchKernelGGL(k_finish1, dim3(1), dim3(1024), (size_t)kw * sizeof(double), s, tmp, S, k, d, tot, Cnext,
+                           ctl, pass, tol, flags, stop);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_finish, dim3(k), dim3(256), 0, s, tmp, S, k, d, tot, Cnext, flags, stop);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !(flags & KM_FIN_UPDATE)) return e;
+    hipLaunchKernelGGL(k_stats, dim3(1), dim3(256), 0, s, tot, k, d, Cnext, ctl, pass, tol, stop);
     return hipGetLastError();
 }
 
 // Spherical k-means: each centre divided by its length (float32 division by the float32-rounded norm, which is
-// summed in float64), a zero centre left as is. pass < 0 runs unconditionally (the start of a fit).
-__global__ __launch_bounds__(64) void k_normalise(float *__restrict__ C, int k, int d,
-                                                  const km_control *__restrict__ ctl, int pass) {
-    if (pass >= 0 && (ctl->iter != pass + 1 || ctl->need_reloc)) return;
+// summed in float64), a zero centre left as is.
+__global__ __launch_bounds__(64) void k_normalise(float *__restrict__ C, int k, int d) {
     const int c = blockIdx.x;
     if (c >= k) return;
     float *row = C + (size_t)c * d;
@@ -359,7 +442,7 @@ __global__ __launch_bounds__(64) void k_normalise(float *__restrict__ C, int k, 
         for (int j = threadIdx.x; j < d; j += 64) row[j] = row[j] / nrm;
 }
 
-hipError_t km_launch_normalise(float *C, int k, int d, const km_control *ctl, int pass, hipStream_t s) {
-    hipLaunchKernelGGL(k_normalise, dim3(k), dim3(64), 0, s, C, k, d, ctl, pass);
+hipError_t km_launch_normalise(float *C, int k, int d, hipStream_t s) {
+    hipLaunchKernelGGL(k_normalise, dim3(k), dim3(64), 0, s, C, k, d);
     return hipGetLastError();
 }

@@ -21,27 +21,16 @@ struct km_control {
 
 // Kernel ids for timing (order fixed; names in km_kernel_names).
 enum km_kernel_id {
-    KK_PREP = 0,
-    KK_ASSIGN_ROWS,
+    KK_ASSIGN_ROWS = 0,
     KK_ACCUM_GENERIC,
     KK_REDUCE,
-    KK_UPDATE_STATS,
-    KK_UPDATE_CENTRES,
+    KK_FINISH,
     KK_NORMALISE,
     KK_FUSED_ROWS,
     KK_FUSED_MFMA,
-    KK_ASSIGN_MFMA,
     KK_COUNT
 };
 extern const char *const km_kernel_names[KK_COUNT];
-
-// Per-pass centre-derived data for the screens.
-struct km_centre_aux {
-    float *csq;      // (kpad) |c|^2 rounded to float32 (+inf for padding centres)
-    float *cnorm;    // (kpad) |c| rounded up
-    float *maxes;    // [0] max |c|, [1] max |c|^2 over real centres
-    uint16_t *cb;    // (kpad, dpad) bf16 of -2*c in the MFMA operand layout, or null
-};
 
 // ---- launchers (defined in the kernel translation units) ----
 // Generic exact assignment (direct form over every centre). labels/best may be null. stop: gate or null.
@@ -61,21 +50,18 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
                                    const uint32_t *labels, const float *best, int k, float *psum,
                                    float *pcomp, int rb0, const int32_t *stop, hipStream_t s);
 
-// Partials (nrb, k*w) sum+comp -> totals (k*w) float64 in a fixed order; tmp holds km_reduce_tmp_doubles.
-size_t km_reduce_tmp_doubles(int nrb, int64_t kw);
-hipError_t km_launch_reduce(const float *psum, const float *pcomp, int nrb, int64_t kw, double *tmp, double *tot,
-                            const int32_t *stop, hipStream_t s);
+// Partials (nrb, k*w) sum+comp -> float64 sums of S = km_reduce_splits(nrb, k*w) fixed ranges: tmp (S, k*w).
+int km_reduce_splits(int nrb, int64_t kw);
+hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
+                                  const int32_t *stop, hipStream_t s);
 
-// Update stage. stats: counts, inertia, empties, argmax, tol test; centres: C <- sums / counts.
-hipError_t km_launch_update_stats(const double *tot, int k, int w, km_control *ctl, int pass, double tol,
-                                  hipStream_t s);
-hipError_t km_launch_update_centres(const double *tot, int k, int d, km_control *ctl, int pass, float *C,
-                                    hipStream_t s);
-hipError_t km_launch_normalise(float *C, int k, int d, const km_control *ctl, int pass, hipStream_t s);
-
-// Centre-derived data for the MFMA screen; also zero-fills nothing. kpad/dpad: padded sizes.
-hipError_t km_launch_prep(const float *C, int k, int d, int kpad, int dpad, km_centre_aux aux,
-                          const int32_t *stop, hipStream_t s);
+// Range sums -> totals (k, d+2). With KM_FIN_UPDATE also the new centres into Cnext and the pass statistics and
+// stopping rule into ctl (pass `pass`, tolerance tol); KM_FIN_SPHERICAL renormalises the new centres.
+#define KM_FIN_UPDATE 1
+#define KM_FIN_SPHERICAL 2
+hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,
+                            int pass, double tol, int flags, const int32_t *stop, hipStream_t s);
+hipError_t km_launch_normalise(float *C, int k, int d, hipStream_t s);
 
 // MFMA-screened exact assignment. Fused variant also accumulates into partials (one row-block per block).
 struct km_mfma_plan {
@@ -88,8 +74,8 @@ struct km_mfma_plan {
 };
 km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused);
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int fused, const float *X, int64_t n, int d, const float *C,
-                          int k, km_centre_aux aux, uint32_t *labels, float *best, float *psum, float *pcomp,
-                          int rb0, km_control *ctl, const int32_t *stop, hipStream_t s);
+                          int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
+                          const int32_t *stop, hipStream_t s);
 
 // Fused single-read pass for dims <= 16: exact rows loop + deterministic accumulation into per-block partials.
 struct km_lowd_plan {

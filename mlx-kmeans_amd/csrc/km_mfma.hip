@@ -28,102 +28,6 @@
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// ------------------------------------------------------------------ centre preparation
-
-// csq (float32 of the float64 sum), cnorm (|c| rounded up), padding centres get csq = 3e38 (never a
-// candidate, and finite so packed keys stay ordered numbers), and the MFMA A operand. For centre tile t and
-// K-step s < DS: cb[((t * (DS+1) + s) * 64 + lane) * 8 + q] = bf16(-2 * C[32t + (lane & 31), (lane >> 5) * DH + 8s + q]).
-// K-step DS carries |c|^2 as two bf16 pieces (q = 0, 1 of the half-0 lanes) against a B operand of ones, so the
-// screen value |c|^2 - 2 x.c comes out of the matrix cores with no accumulator initialisation.
-__global__ __launch_bounds__(256) void k_prep(const float *__restrict__ C, int k, int d, int kpad, int dpad,
-                                              float *__restrict__ csq, float *__restrict__ cnorm,
-                                              uint16_t *__restrict__ cb, const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int DS = dpad / 16, DH = dpad / 2;
-    const int64_t total = (int64_t)kpad * (dpad + 16);
-    if (e < total) {
-        const int q = (int)(e & 7);
-        const int lane = (int)((e >> 3) & 63);
-        const int64_t ts = e >> 9;
-        const int s = (int)(ts % (DS + 1)), t = (int)(ts / (DS + 1));
-        const int c = 32 * t + (lane & 31);
-        float v = 0.0f;
-        if (s < DS) {
-            const int j = (lane >> 5) * DH + 8 * s + q;
-            if (c < k && j < d) v = -2.0f * C[(size_t)c * d + j];
-        } else if ((lane >> 5) == 0 && q < 2) {
-            double sq = 3.0e38;
-            if (c < k) {
-                sq = 0.0;
-                for (int j = 0; j < d; j++) {
-                    const double x = C[(size_t)c * d + j];
-                    sq += x * x;
-                }
-            }
-            const float sf = (float)sq;
-            const float hi = (float)(__bf16)sf;
-            v = (q == 0) ? hi : (sf - hi);
-        }
-        __bf16 b = (__bf16)v;
-        cb[e] = *reinterpret_cast<uint16_t *>(&b);
-    }
-    if (e < kpad) {
-        const int c = (int)e;
-        if (c < k) {
-            double sq = 0.0;
-            for (int j = 0; j < d; j++) {
-                const double x = C[(size_t)c * d + j];
-                sq += x * x;
-            }
-            csq[c] = (float)sq;
-            cnorm[c] = (float)(sqrt(sq) * (1.0 + 1e-6));
-        } else {
-            csq[c] = 3.0e38f;
-            cnorm[c] = 0.0f;
-        }
-    }
-}
-
-// maxes[0] = max |c| (rounded up), maxes[1] = max |c|^2 over the real centres.
-__global__ __launch_bounds__(256) void k_prep_max(const float *__restrict__ csq, const float *__restrict__ cnorm,
-                                                  int k, float *__restrict__ maxes,
-                                                  const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    __shared__ float a[256], b[256];
-    float mn = 0.0f, ms = 0.0f;
-    for (int c = threadIdx.x; c < k; c += 256) {
-        mn = fmaxf(mn, cnorm[c]);
-        ms = fmaxf(ms, csq[c]);
-    }
-    a[threadIdx.x] = mn;
-    b[threadIdx.x] = ms;
-    __syncthreads();
-    for (int h = 128; h > 0; h >>= 1) {
-        if ((int)threadIdx.x < h) {
-            a[threadIdx.x] = fmaxf(a[threadIdx.x], a[threadIdx.x + h]);
-            b[threadIdx.x] = fmaxf(b[threadIdx.x], b[threadIdx.x + h]);
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        maxes[0] = a[0];
-        maxes[1] = b[0];
-    }
-}
-
-hipError_t km_launch_prep(const float *C, int k, int d, int kpad, int dpad, km_centre_aux aux,
-                          const int32_t *stop, hipStream_t s) {
-    const int64_t total = (int64_t)kpad * (dpad + 16);
-    const int64_t m = total > kpad ? total : kpad;
-    hipLaunchKernelGGL(k_prep, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, C, k, d, kpad, dpad, aux.csq,
-                       aux.cnorm, aux.cb, stop);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_prep_max, dim3(1), dim3(256), 0, s, aux.csq, aux.cnorm, k, aux.maxes, stop);
-    return hipGetLastError();
-}
-
 // ------------------------------------------------------------------ the fused kernel
 //
 // Exactness of the screen. For a row x and centre c let A_c = |c|^2 - 2 x.c (exact reals) and D_c = |x - c|^2 =
@@ -327,10 +231,9 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
 
 template <int D, int KP, int WAVES, bool ACCUM>
 __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
-    const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k, const float *__restrict__ maxes,
-    const uint16_t *__restrict__ cbg, int64_t rbs, uint32_t *__restrict__ labels, float *__restrict__ best,
-    float *__restrict__ psum, float *__restrict__ pcomp, int rb0, km_control *__restrict__ ctl,
-    const int32_t *__restrict__ stop) {
+    const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k, int64_t rbs,
+    uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
+    int rb0, km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
     using G = Geo<D, KP>;
     using L = Lay<D>;
     constexpr int DH = G::DH, DS = G::DS, KT = G::KT, CS = G::CS, W = D + 2;
@@ -353,7 +256,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 
     extern __shared__ float lds[];
     float *Cl = lds;                                  // KP x CS float32 centres
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     char *wbase = reinterpret_cast<char *>(lds + KP * CS) + wave * WBYTES;
     uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * L::BUF);   // labels of the block (0x4000: no row)
 
@@ -367,17 +270,48 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         Cl[e] = (c < k && j < D) ? C[(size_t)c * D + j] : 0.0f;
     }
     const int h = lane >> 5, ln = lane & 31;
+    __syncthreads();
+    // The screen's A operand from the float32 centres: for centre tile t and K-step s < DS, lane (h, ln) holds
+    // bf16(-2 c[32t + ln][h*DH + 8s + q]); K-step DS carries |c|^2 (float32 of the float64 sum over dims
+    // ascending; 3e38 for padding centres, never a candidate and finite so packed keys stay ordered) as two bf16
+    // pieces against a B operand of ones, so |c|^2 - 2 x.c comes out of the matrix cores directly. The window
+    // needs max |c| (rounded up) and max |c|^2 over the real centres.
     bf16x8 Aop[KT][DS + 1];
+    float cn_l = 0.0f, cs_l = 0.0f;
 #pragma unroll
-    for (int t = 0; t < KT; t++)
+    for (int t = 0; t < KT; t++) {
+        const int cA = 32 * t + ln;
+        const bool real = cA < k;
+        double sq = 0.0;
+        if (real)
+            for (int j = 0; j < D; j++) {
+                const double v = Cl[cA * CS + j];
+                sq += v * v;
+            }
+        const float sf = real ? (float)sq : 3.0e38f;
+        if (real) {
+            cn_l = fmaxf(cn_l, (float)(sqrt(sq) * (1.0 + 1e-6)));
+            cs_l = fmaxf(cs_l, sf);
+        }
 #pragma unroll
-        for (int s = 0; s <= DS; s++)
-            Aop[t][s] = *reinterpret_cast<const bf16x8 *>(cbg + ((size_t)(t * (DS + 1) + s) * 64 + lane) * 8);
+        for (int st = 0; st < DS; st++)
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int j = h * DH + 8 * st + q;
+                Aop[t][st][q] = (__bf16)((real && j < D) ? -2.0f * Cl[cA * CS + j] : 0.0f);
+            }
+        const float hi = (float)(__bf16)sf;
+#pragma unroll
+        for (int q = 0; q < 8; q++) Aop[t][DS][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        cn_l = fmaxf(cn_l, __shfl_xor(cn_l, off));
+        cs_l = fmaxf(cs_l, __shfl_xor(cs_l, off));
+    }
+    const float cnmax = cn_l, csqmax = cs_l;
     bf16x8 Bone;
 #pragma unroll
     for (int q = 0; q < 8; q++) Bone[q] = (__bf16)((h == 0 && q < 2) ? 1.0f : 0.0f);
-    const float cnmax = maxes[0], csqmax = maxes[1];
-    __syncthreads();
 
     float ine_s = 0.0f, ine_c = 0.0f;   // Kahan inertia of this lane's rows
     uint32_t fallback = 0;
@@ -679,8 +613,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 
 // ------------------------------------------------------------------ planning and launch
 
-typedef void (*fused_fn)(const float *, int64_t, const float *, int, const float *, const uint16_t *, int64_t,
-                         uint32_t *, float *, float *, float *, int, km_control *, const int32_t *);
+typedef void (*fused_fn)(const float *, int64_t, const float *, int, int64_t, uint32_t *, float *, float *, float *,
+                         int, km_control *, const int32_t *);
 
 // One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
 struct fused_entry {
@@ -764,12 +698,12 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused) {
 }
 
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int fused, const float *X, int64_t n, int d, const float *C, int k,
-                          km_centre_aux aux, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0,
-                          km_control *ctl, const int32_t *stop, hipStream_t s) {
+                          uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
+                          const int32_t *stop, hipStream_t s) {
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
     fused_fn fn = pl.waves == 4 ? (fused ? fe->acc4 : fe->noacc4) : (fused ? fe->acc2 : fe->noacc2);
-    hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, aux.maxes, aux.cb, pl.rbs,
-                       labels, best, psum, pcomp, rb0, ctl, stop);
+    hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, pl.rbs, labels, best, psum,
+                       pcomp, rb0, ctl, stop);
     return hipGetLastError();
 }
