@@ -31,9 +31,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // ------------------------------------------------------------------ the fused kernel
 //
 // Exactness of the screen. For a row x and centre c let A_c = |c|^2 - 2 x.c (exact reals) and D_c = |x - c|^2 =
-// |x|^2 + A_c. The matrix cores give a'_c; with bf16 rounding of x and c (relative 2^-9 each), the float32
-// accumulation of DP + 2 products (gamma_{DP+2}), the two-piece |c|^2 (2^-17) and bf16 denormal flushing,
-//     |a'_c - A_c| <= E = BETA |x| max|c| + GAM2 max|c|^2 + FLUSH (|x| + max|c|) + TINY      (uniform in c).
+// |x|^2 + A_c. The matrix cores give a'_c = sum_j bf16(x_j) (h_j + l_j) + q_h + q_l, where h_j + l_j is -2 c_j split
+// into two bf16 pieces (h = bf16(-2c_j), l = bf16(-2c_j - h): relative residual 2^-16) and q_h + q_l is |c|^2 the
+// same way. bf16 rounding to nearest has unit roundoff u = 2^-8 (1 + 2^-8 rounds to 1), so bf16(x_j) = x_j (1 + d),
+// |d| <= 2^-8; products of bf16 values are exact in float32 and the float32 accumulation of NACC = 2 DP + 2 terms
+// adds at most gamma_NACC times their absolute sum. With bf16 denormal flushing covered by FLUSH,
+//     |a'_c - A_c| <= E = BETA |x| max|c| + GAM2 max|c|^2 + FLUSH (|x| + max|c|) + TINY      (uniform in c),
+//     BETA = 2 (2^-8 + 2^-16 + 2^-24) + 2.04 gamma_NACC,   GAM2 = 1.01 gamma_NACC + 2^-16 + 2^-23.
 // The float32 direct form s_c of the rows loop satisfies |s_c - D_c| <= g D_c + eta, g = gamma_{D+2}. A centre c
 // can hold the row's minimum only if s_c <= s_m for the screen's minimiser m, which forces
 //     a'_c - a'_m <= 2E + 2 g/(1-g) D_m + tiny,   D_m <= |x|^2 + a'_m + E,
@@ -42,6 +46,14 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // their low IB mantissa bits (a relative perturbation of at most RHO), which the test absorbs.
 
 __device__ __forceinline__ uint32_t u32(float v) { return __float_as_uint(v); }
+
+// v_min_f32 as written: fminf would first canonicalise each input (one more instruction per screen value). A key
+// that is NaN (non-finite data) makes the row's minimum NaN, and such a row takes the full scan.
+__device__ __forceinline__ float vmin(float a, float b) {
+    float r;
+    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float f32(uint32_t v) { return __uint_as_float(v); }
 
 // v_permlane32_swap: lane l < 32 gets (va of lane l, va of lane l+32); lane l >= 32 gets (vb of lane l-32,
@@ -70,7 +82,8 @@ template <int D, int KP>
 struct Geo {
     static constexpr int DP = (D + 15) / 16 * 16;   // padded dims
     static constexpr int DH = DP / 2;               // dims per lane half
-    static constexpr int DS = DP / 16;              // MFMA K-steps over the dims (one more carries |c|^2)
+    static constexpr int DS = DP / 16;              // MFMA K-steps over the dims
+    static constexpr int AK = 2 * DS + 1;           // A-operand K-steps: high pieces, low pieces, |c|^2
     static constexpr int KT = KP / 32;              // centre tiles
     static constexpr int IB = KT <= 1 ? 4 : KT <= 2 ? 5 : 6;   // index bits packed into keys (16 KT values)
     static constexpr int CS = D + 4;                // LDS row stride of the float32 centres
@@ -80,7 +93,7 @@ struct Geo {
 // Screen one 32-row tile: x is this lane's half row. Returns the smallest and second smallest packed key over
 // this lane's 16 KT screen values.
 template <int D, int KP>
-__device__ __forceinline__ void screen_tile(const float (&x)[Geo<D, KP>::DH], const bf16x8 (&Aop)[Geo<D, KP>::KT][Geo<D, KP>::DS + 1],
+__device__ __forceinline__ void screen_tile(const float (&x)[Geo<D, KP>::DH], const bf16x8 (&Aop)[Geo<D, KP>::KT][Geo<D, KP>::AK],
                                             const bf16x8 &Bone, f32x16 (&a)[Geo<D, KP>::KT]) {
     using G = Geo<D, KP>;
     bf16x8 B[G::DS];
@@ -94,7 +107,10 @@ __device__ __forceinline__ void screen_tile(const float (&x)[Geo<D, KP>::DH], co
         a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][0], B[0], zero, 0, 0, 0);
 #pragma unroll
         for (int s = 1; s < G::DS; s++) a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][s], B[s], a[t], 0, 0, 0);
-        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][G::DS], Bone, a[t], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < G::DS; s++)
+            a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][G::DS + s], B[s], a[t], 0, 0, 0);
+        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][2 * G::DS], Bone, a[t], 0, 0, 0);
     }
 }
 
@@ -110,7 +126,7 @@ __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], flo
         for (int v = 0; v < 16; v++) {
             const float key = f32((u32(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
             m2 = __builtin_amdgcn_fmed3f(m1, m2, key);
-            m1 = fminf(m1, key);
+            m1 = vmin(m1, key);
         }
 }
 
@@ -242,8 +258,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     // per wave: two block buffers + 64 uint16 labels during the loop, the fold after it
     constexpr int WBYTES = (2 * L::BUF + 128 > FOLD) ? 2 * L::BUF + 128 : FOLD;
     // window constants
-    constexpr float BETA = (float)(2.0 * (0x1p-8 + 0x1p-18) * (1.0 + 0x1p-20) + 2.01 * km_gamma(G::DP + 2));
-    constexpr float GAM2 = (float)(km_gamma(G::DP + 2) + 0x1p-17);
+    constexpr int NACC = 2 * G::DP + 2;
+    constexpr float BETA = (float)((2.0 * (0x1p-8 + 0x1p-16 + 0x1p-24) + 2.04 * km_gamma(NACC)) * (1.0 + 0x1p-20));
+    constexpr float GAM2 = (float)((1.01 * km_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
     constexpr float GDIR = (float)(km_gamma(D + 2) / (1.0 - km_gamma(D + 2)) * (1.0 + 0x1p-20));
     constexpr float RHO = (float)(1.01 * (double)(1 << G::IB) * 0x1p-23);
     constexpr float FLUSH = (float)(0x1p-123 * 16.0);
@@ -272,11 +289,12 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     const int h = lane >> 5, ln = lane & 31;
     __syncthreads();
     // The screen's A operand from the float32 centres: for centre tile t and K-step s < DS, lane (h, ln) holds
-    // bf16(-2 c[32t + ln][h*DH + 8s + q]); K-step DS carries |c|^2 (float32 of the float64 sum over dims
-    // ascending; 3e38 for padding centres, never a candidate and finite so packed keys stay ordered) as two bf16
-    // pieces against a B operand of ones, so |c|^2 - 2 x.c comes out of the matrix cores directly. The window
-    // needs max |c| (rounded up) and max |c|^2 over the real centres.
-    bf16x8 Aop[KT][DS + 1];
+    // the high bf16 piece of -2 c[32t + ln][h*DH + 8s + q], and K-step DS + s the low piece (the bf16 residual);
+    // K-step 2 DS carries |c|^2 (float32 of the float64 sum over dims ascending; 3e38 for padding centres, never a
+    // candidate and finite so packed keys stay ordered) as two bf16 pieces against a B operand of ones, so
+    // |c|^2 - 2 x.c comes out of the matrix cores directly. The window needs max |c| (rounded up) and max |c|^2
+    // over the real centres.
+    bf16x8 Aop[KT][G::AK];
     float cn_l = 0.0f, cs_l = 0.0f;
 #pragma unroll
     for (int t = 0; t < KT; t++) {
@@ -298,11 +316,14 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 #pragma unroll
             for (int q = 0; q < 8; q++) {
                 const int j = h * DH + 8 * st + q;
-                Aop[t][st][q] = (__bf16)((real && j < D) ? -2.0f * Cl[cA * CS + j] : 0.0f);
+                const float v = (real && j < D) ? -2.0f * Cl[cA * CS + j] : 0.0f;
+                const __bf16 vh = (__bf16)v;
+                Aop[t][st][q] = vh;
+                Aop[t][DS + st][q] = (__bf16)(v - (float)vh);
             }
         const float hi = (float)(__bf16)sf;
 #pragma unroll
-        for (int q = 0; q < 8; q++) Aop[t][DS][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
+        for (int q = 0; q < 8; q++) Aop[t][2 * DS][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
     }
     for (int off = 32; off > 0; off >>= 1) {
         cn_l = fmaxf(cn_l, __shfl_xor(cn_l, off));
