@@ -51,7 +51,13 @@ struct Part {
     float *owned;     // non-null when the context allocated X
     int64_t rows;
     bool aligned;     // 16-byte aligned: whole-float4 row loads are allowed
+    uint16_t *x16 = nullptr;   // the wide-row path's bf16 row operands (built on first use)
+    float *xsq = nullptr;      // |x|^2 rounded up per row (built with x16)
+    int x16_ds = 0;            // K-steps x16 was built for
 };
+
+// Which kernel family ran a pass (the public path code is coarser: both MFMA families report KM_PATH_MFMA).
+enum km_family { FAM_NONE = 0, FAM_ROWS, FAM_MFMA_FUSED, FAM_LOWD, FAM_BIG };
 
 struct ProfRec {
     int kernel;
@@ -66,6 +72,12 @@ struct km_ctx {
     int64_t n = 0;
     std::string err;
     int32_t last_path = 0;
+    int last_family = FAM_NONE;
+    DBuf<uint16_t> cop;     // wide-row path: bf16 centre operands
+    DBuf<float> bcsq, bcn, bmax;
+    DBuf<uint16_t> ncand;
+    DBuf<uint16_t> cand;
+    DBuf<uint32_t> hist, counts, base, perm, over;
     DBuf<float> Cb[2];      // centre buffers (k, d): pass p reads Cb[p & 1], writes Cb[(p + 1) & 1]
     DBuf<float> psum, pcomp;
     DBuf<double> tot;
@@ -163,8 +175,11 @@ extern "C" km_ctx *km_create(int32_t device) {
 }
 
 static void drop_parts(km_ctx *c) {
-    for (auto &p : c->parts)
+    for (auto &p : c->parts) {
         if (p.owned) (void)hipFree(p.owned);
+        if (p.x16) (void)hipFree(p.x16);
+        if (p.xsq) (void)hipFree(p.xsq);
+    }
     c->parts.clear();
     c->n = 0;
     c->d = 0;
@@ -181,6 +196,17 @@ extern "C" void km_destroy(km_ctx *c) {
     c->pcomp.release();
     c->tot.release();
     c->tot2.release();
+    c->cop.release();
+    c->bcsq.release();
+    c->bcn.release();
+    c->bmax.release();
+    c->ncand.release();
+    c->cand.release();
+    c->hist.release();
+    c->counts.release();
+    c->base.release();
+    c->perm.release();
+    c->over.release();
     c->red.release();
     c->labels.release();
     c->best.release();
@@ -200,7 +226,11 @@ extern "C" const char *km_last_error(const km_ctx *c) { return c ? c->err.c_str(
 static int add_part(km_ctx *c, const float *X, int64_t rows, int32_t where) {
     if (!X) return fail(c, KM_EINVAL, "data pointer is null");
     if (rows < 1) return fail(c, KM_EINVAL, "expected a nonempty 2-D (rows, dims) array, got %lld rows", (long long)rows);
-    Part p{nullptr, nullptr, rows, true};
+    Part p;
+    p.X = nullptr;
+    p.owned = nullptr;
+    p.rows = rows;
+    p.aligned = true;
     if (where == KM_DEVICE) {
         p.X = X;
         p.aligned = ((uintptr_t)X % 16) == 0;
@@ -272,17 +302,30 @@ static bool parts_aligned(const km_ctx *c) {
     return true;
 }
 
+static bool big_ok(const km_ctx *c, int k) {
+    for (auto &p : c->parts)
+        if (!km_plan_big(p.rows, c->d, k).ok) return false;
+    return !c->parts.empty();
+}
+
+// Returns the kernel family for this pass (FAM_*), or -1 when an explicit path does not serve the shape.
 static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
     const bool al = parts_aligned(c);
     *mp = km_plan_mfma(c->n, c->d, k, 1);
     if (!al) mp->ok = 0;
     const bool lowd_ok = km_plan_lowd(c->n, c->d, k, al).ok != 0;
-    if (path == KM_PATH_ROWS) return KM_PATH_ROWS;
-    if (path == KM_PATH_MFMA) return mp->ok ? KM_PATH_MFMA : -1;
-    if (path == KM_PATH_FUSED) return lowd_ok ? KM_PATH_FUSED : -1;
-    if (mp->ok && c->d >= 16 && (int64_t)k * c->d >= 256) return KM_PATH_MFMA;
-    if (lowd_ok) return KM_PATH_FUSED;
-    return KM_PATH_ROWS;
+    const bool wide_ok = big_ok(c, k);
+    if (path == KM_PATH_ROWS) return FAM_ROWS;
+    if (path == KM_PATH_MFMA) return mp->ok ? FAM_MFMA_FUSED : wide_ok ? FAM_BIG : -1;
+    if (path == KM_PATH_FUSED) return lowd_ok ? FAM_LOWD : -1;
+    if (mp->ok && c->d >= 16 && (int64_t)k * c->d >= 256) return FAM_MFMA_FUSED;
+    if (lowd_ok) return FAM_LOWD;
+    if (wide_ok && (int64_t)k * c->d >= 1024) return FAM_BIG;
+    return FAM_ROWS;
+}
+
+static int32_t family_path(int fam) {
+    return fam == FAM_ROWS ? KM_PATH_ROWS : fam == FAM_LOWD ? KM_PATH_FUSED : KM_PATH_MFMA;
 }
 
 // Sizes the per-pass workspaces. Returns KM_OK or an error.
@@ -301,15 +344,91 @@ static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bo
 }
 
 // Partials -> totals in c->tot, and with KM_FIN_UPDATE the new centres into Cb[(pass + 1) & 1] and the pass
-// statistics into the control block.
-static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags, const int32_t *stop) {
+// statistics into the control block. presummed > 0: c->red already holds that many range sums.
+static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags, const int32_t *stop,
+                       int presummed = 0) {
     const int d = c->d;
     const int64_t kw = (int64_t)k * (d + 2);
-    const int S = km_reduce_splits(rb, kw);
-    HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce_split(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, stop, c->stream); }));
+    int S = presummed;
+    if (!presummed) {
+        S = km_reduce_splits(rb, kw);
+        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce_split(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, stop, c->stream); }));
+    }
     float *Cn = c->Cb[(pass + 1) & 1].p;
     HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, S, k, d, c->tot.p, Cn, c->ctl, pass, tol, flags, stop, c->stream); }));
     return KM_OK;
+}
+
+// The wide-row pass: centre operands, then per slice the screen + exact rescoring (labels and best for every
+// row) and the sorted accumulation into one range sum per slice, then the finish.
+static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d, const int32_t *stop, int pass,
+                   double tol, int flags) {
+    const int d = c->d;
+    const int64_t kw = (int64_t)k * (d + 2);
+    const float *Cin = c->Cb[pass & 1].p;
+    int64_t max_rows = 0;
+    int max_nb = 0;
+    for (auto &p : c->parts) {
+        const km_big_plan bp = km_plan_big(p.rows, d, k);
+        max_rows = std::max(max_rows, p.rows);
+        max_nb = std::max(max_nb, bp.nb);
+        if (!p.x16 || p.x16_ds != bp.DS) {
+            if (p.x16) (void)hipFree(p.x16);
+            if (p.xsq) (void)hipFree(p.xsq);
+            p.x16 = nullptr;
+            p.xsq = nullptr;
+            HIPCHK(c, hipMalloc((void **)&p.x16, km_big_x16_elems(bp) * sizeof(uint16_t)));
+            HIPCHK(c, hipMalloc((void **)&p.xsq, (size_t)p.rows * 2 * sizeof(float)));
+            HIPCHK(c, launch(c, KK_BIG_PREP, [&] { return km_launch_big_rows(bp, p.X, p.rows, d, p.x16, p.xsq, c->stream); }));
+            p.x16_ds = bp.DS;
+        }
+    }
+    const km_big_plan bp0 = km_plan_big(max_rows, d, k);
+    HIPCHK(c, c->cop.ensure(km_big_cop_elems(bp0)));
+    HIPCHK(c, c->bcsq.ensure(bp0.kpad));
+    HIPCHK(c, c->bcn.ensure((size_t)bp0.kpad * 2));
+    HIPCHK(c, c->bmax.ensure(4));
+    HIPCHK(c, c->ncand.ensure((size_t)max_rows));
+    HIPCHK(c, c->cand.ensure((size_t)max_rows * 32));
+    HIPCHK(c, c->hist.ensure((size_t)max_nb * k));
+    HIPCHK(c, c->counts.ensure((size_t)k));
+    HIPCHK(c, c->base.ensure((size_t)k));
+    HIPCHK(c, c->perm.ensure((size_t)max_rows));
+    HIPCHK(c, c->over.ensure((size_t)max_rows));
+    HIPCHK(c, c->labels.ensure((size_t)c->n));
+    HIPCHK(c, c->best.ensure((size_t)c->n));
+    HIPCHK(c, c->tot.ensure((size_t)kw));
+    const int S = (int)c->parts.size();
+    HIPCHK(c, c->red.ensure((size_t)S * kw));
+    uint32_t *lab_all = labels_d ? labels_d : c->labels.p;
+    float *best_all = best_d ? best_d : c->best.p;
+    HIPCHK(c, launch(c, KK_BIG_PREP, [&] {
+        return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop, c->stream);
+    }));
+    int64_t row0 = 0;
+    for (size_t i = 0; i < c->parts.size(); i++) {
+        const Part &p = c->parts[i];
+        const km_big_plan bp = km_plan_big(p.rows, d, k);
+        if (i > 0)   // each slice lists its own overflow rows
+            HIPCHK(c, launch(c, KK_BIG_PREP, [&] {
+                return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop,
+                                             c->stream);
+            }));
+        HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
+            return km_launch_big_screen(bp, mode, p.x16, p.xsq, p.rows, d, c->cop.p, c->bmax.p, k, c->ncand.p,
+                                        c->cand.p, c->over.p, c->ctl, stop, c->stream);
+        }));
+        HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {
+            return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->ctl,
+                                         lab_all + row0, best_all + row0, stop, c->stream);
+        }));
+        HIPCHK(c, launch(c, KK_BIG_ACCUM, [&] {
+            return km_launch_big_accum(bp, p.X, p.rows, d, lab_all + row0, best_all + row0, k, c->hist.p,
+                                       c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw, stop, c->stream);
+        }));
+        row0 += p.rows;
+    }
+    return finish_pass(c, k, 0, pass, tol, flags, stop, S);
 }
 
 // Pass `pass`: assignment + accumulation over every slice with the centres in Cb[pass & 1], then the finish
@@ -321,16 +440,19 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
     HIPCHK(c, c->Cb[(pass + 1) & 1].ensure((size_t)k * c->d));
     const float *Cin = c->Cb[pass & 1].p;
     km_mfma_plan mp;
-    const int chosen = choose_path(c, k, path, &mp);
-    if (chosen < 0)
+    const int fam = choose_path(c, k, path, &mp);
+    if (fam < 0)
         return fail(c, KM_EINVAL, "path=%s does not serve k=%d, dims=%d on this build",
                     path == KM_PATH_MFMA ? "mfma" : "fused", k, c->d);
-    c->last_path = chosen;
+    c->last_path = family_path(fam);
+    c->last_family = fam;
+    const int chosen = c->last_path;
     const int32_t *stop = gated ? &c->ctl->stop : nullptr;
     const int d = c->d;
-    const int64_t kw = (int64_t)k * (d + 2);
 
-    if (chosen == KM_PATH_MFMA) {
+    if (fam == FAM_BIG) return run_big(c, k, mode, labels_d, best_d, stop, pass, tol, flags);
+
+    if (fam == FAM_MFMA_FUSED) {
         size_t total_rb = 0;
         std::vector<km_mfma_plan> plans;
         for (auto &p : c->parts) {
@@ -355,7 +477,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         return finish_pass(c, k, rb, pass, tol, flags, stop);
     }
 
-    if (chosen == KM_PATH_FUSED) {
+    if (fam == FAM_LOWD) {
         size_t total_rb = 0;
         std::vector<km_lowd_plan> plans;
         const bool al = parts_aligned(c);
@@ -461,7 +583,7 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
     const int64_t kw = (int64_t)k * w;
     HIPCHK(c, hipMemcpyAsync(totals, c->tot.p, kw * sizeof(double), hipMemcpyDeviceToHost, c->stream));
     std::vector<double> cb2;
-    if (c->last_path == KM_PATH_MFMA) {
+    if (c->last_family == FAM_MFMA_FUSED) {
         // The fused screen keeps the per-cluster sums of x but only the pass total of best (column 1 of
         // cluster 0). The per-cluster best sums come from one more deterministic accumulation over the
         // [count, best] columns alone, reading the labels and best this pass wrote.

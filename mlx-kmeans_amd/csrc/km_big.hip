@@ -1,0 +1,890 @@
+// Exact Lloyd pass for wide rows (16 < dims <= 768, k <= 4096): the reference's "tiles" design (core.py:616-651,
+// 310-377: matrix-unit dot products, an error margin, exact rescoring of the candidates) rebuilt for CDNA4, plus
+// its sorted accumulation (core.py:934-994, 424-449, 1421-1441).
+//
+//   k_big_rows      once per dataset: the rows as bf16 MFMA B operands, X16T[tile][K-step][lane][8] (coalesced
+//                   1 KB per wave per K-step), and |x|^2 rounded up per row
+//   k_big_centres   per pass: the centres as bf16 MFMA A operands, Cop[chunk][K-step][lane][8], with one extra
+//                   K-step carrying |c|^2 against a B operand of ones; |c| (rounded up) and |c|^2 per centre
+//   k_big_screen    a'_c = |c|^2 - 2 x.c for every (row, centre) on the matrix cores, never stored, twice: the
+//                   first pass finds each row's smallest packed key (value, centre index), the second lists the
+//                   centres inside the error window around it - every centre that can hold the exact minimum
+//   k_big_rescore   the rows loop (core.py:263-274) on those candidates only, ascending index, strict '<'
+//   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every centre
+//   k_big_hist/scan/scatter/segsum   a stable counting sort of the rows by label and per-cluster sums in row
+//                   order (float64), the totals of the pass
+//
+// Labels and best are the rows loop's bit for bit (see the window below). With mode KM_APPROX the screen's
+// minimiser is taken on trust, as the reference's exact=False path does (core.py:878-890, 1061-1088), only its
+// distance is computed exactly, and the screen runs once.
+#pragma clang fp contract(off)
+#include "km_internal.h"
+#include "kmeans_hip.h"
+#include <math.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void *lds_vptr;
+typedef __attribute__((address_space(1))) void *gbl_vptr;
+
+static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
+static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
+static constexpr int KB_SLICE = 16;       // A-operand K-steps per LDS slice (16 KB)
+static constexpr int KB_WAVES = 4;        // waves per screen block (32 rows each)
+static constexpr int KB_OVER = 0xffff;    // ncand value: scan every centre
+
+__host__ __device__ constexpr double kb_gamma(int m) {
+    return m * 5.9604644775390625e-08 / (1.0 - m * 5.9604644775390625e-08);
+}
+
+__device__ __forceinline__ uint32_t kb_u32(float v) { return __float_as_uint(v); }
+__device__ __forceinline__ float kb_f32(uint32_t v) { return __uint_as_float(v); }
+__device__ __forceinline__ float kb_min(float a, float b) {
+    float r;
+    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// value of lane l ^ 32
+__device__ __forceinline__ float kb_partner(float v, int lane) {
+    const auto r = __builtin_amdgcn_permlane32_swap(kb_u32(v), kb_u32(v), false, false);
+    return kb_f32(lane < 32 ? r[1] : r[0]);
+}
+__device__ __forceinline__ float kb_u32f(uint32_t v) { return __uint_as_float(v); }
+__device__ __forceinline__ uint32_t kb_f32u(float v) { return __float_as_uint(v); }
+
+// ------------------------------------------------------------------ rows (once per dataset)
+
+// Thread per (tile, K-step, lane): 8 bf16 of row 32 tile + (lane & 31), dims 16 s + 8 (lane >> 5) + q.
+__global__ __launch_bounds__(256) void k_big_rows(const float *__restrict__ X, int64_t n, int d, int DS,
+                                                  uint16_t *__restrict__ X16T, int64_t ntiles) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= ntiles * DS * 64) return;
+    const int lane = (int)(e & 63);
+    const int64_t ts = e >> 6;
+    const int s = (int)(ts % DS);
+    const int64_t tile = ts / DS;
+    const int64_t row = tile * 32 + (lane & 31);
+    const int j0 = 16 * s + 8 * (lane >> 5);
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        float a = 0.0f, b = 0.0f;
+        if (row < n) {
+            if (j0 + 2 * p < d) a = X[row * d + j0 + 2 * p];
+            if (j0 + 2 * p + 1 < d) b = X[row * d + j0 + 2 * p + 1];
+        }
+        const __bf16 ha = (__bf16)a, hb = (__bf16)b;
+        w[p] = (uint32_t)(*reinterpret_cast<const uint16_t *>(&ha)) |
+               ((uint32_t)(*reinterpret_cast<const uint16_t *>(&hb)) << 16);
+    }
+    *reinterpret_cast<uint4 *>(X16T + e * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Wave per row: xn[2 row] = |x|^2 and xn[2 row + 1] = |bf16(x) - x| (the norm of the screen operand's rounding
+// residual), float64 sums (dims split over lanes, fixed butterfly) rounded up into float32; +inf when the row is
+// not finite.
+__global__ __launch_bounds__(256) void k_big_xsq(const float *__restrict__ X, int64_t n, int d,
+                                                 float *__restrict__ xn) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    double s = 0.0, r = 0.0;
+    bool fin = true;
+    for (int j = lane; j < d; j += 64) {
+        const float v = X[row * d + j];
+        fin = fin && isfinite(v);
+        s += (double)v * (double)v;
+        const double e = (double)(float)(__bf16)v - (double)v;
+        r += e * e;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        s += __shfl_xor(s, off);
+        r += __shfl_xor(r, off);
+    }
+    const bool all = __all(fin);
+    if (lane == 0) {
+        const bool ok = all && s * (1.0 + 0x1p-20) < 3.0e38;
+        xn[2 * row] = ok ? (float)(s * (1.0 + 0x1p-20)) : INFINITY;
+        xn[2 * row + 1] = ok ? (float)(sqrt(r) * (1.0 + 0x1p-20)) : INFINITY;
+    }
+}
+
+// ------------------------------------------------------------------ centres (per pass)
+
+// Wave per centre: |c|^2 (float64 sum of the float32 values, dims ascending within each lane then a fixed
+// butterfly), |c| rounded up, and |bf16(-2c) + 2c| (the operand's rounding residual) rounded up in cn[kpad + c].
+// Padding centres (k <= c < kpad): csq = 3e38 (never a candidate), cn = 0.
+__global__ __launch_bounds__(256) void k_big_cnorm(const float *__restrict__ C, int k, int kpad, int d,
+                                                   float *__restrict__ csq, float *__restrict__ cn,
+                                                   km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    if (blockIdx.x == 0 && threadIdx.x == 0) ctl->n_over = 0;   // rows the next screen lists for a full scan
+    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (c >= kpad) return;
+    double s = 0.0, r = 0.0;
+    if (c < k)
+        for (int j = lane; j < d; j += 64) {
+            const float v = C[(int64_t)c * d + j];
+            s += (double)v * (double)v;
+            const float m2 = -2.0f * v;
+            const double e = (double)(float)(__bf16)m2 - (double)m2;
+            r += e * e;
+        }
+    for (int off = 32; off > 0; off >>= 1) {
+        s += __shfl_xor(s, off);
+        r += __shfl_xor(r, off);
+    }
+    if (lane == 0) {
+        csq[c] = c < k ? (float)s : 3.0e38f;
+        cn[c] = c < k ? (float)(sqrt(s) * (1.0 + 1e-6)) : 0.0f;
+        cn[kpad + c] = c < k ? (float)(sqrt(r) * (1.0 + 1e-6)) : 0.0f;
+    }
+}
+
+// Thread per (chunk, K-step, lane): Cop for K-step s < DS holds bf16(-2 c[32 chunk + (lane & 31)][16 s + 8 h + q]);
+// K-step DS holds |c|^2 as two bf16 pieces in q = 0, 1 of the h = 0 lanes. One block also writes
+// maxes = {max |c| (rounded up), max |c|^2, max |bf16(-2c) + 2c|} over the real centres.
+__global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C, int k, int d, int DS, int nchunks,
+                                                     const float *__restrict__ csq, const float *__restrict__ cn,
+                                                     uint16_t *__restrict__ Cop, float *__restrict__ maxes,
+                                                     const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int AK = DS + 1;
+    if (e < (int64_t)nchunks * AK * 64) {
+        const int lane = (int)(e & 63);
+        const int64_t cs = e >> 6;
+        const int s = (int)(cs % AK);
+        const int ch = (int)(cs / AK);
+        const int c = 32 * ch + (lane & 31);
+        const int h = lane >> 5;
+        uint16_t out[8];
+        for (int q = 0; q < 8; q++) {
+            float v = 0.0f;
+            if (s < DS) {
+                const int j = 16 * s + 8 * h + q;
+                if (c < k && j < d) v = -2.0f * C[(int64_t)c * d + j];
+            } else if (h == 0 && q < 2) {
+                const float sf = csq[c];
+                const float hi = (float)(__bf16)sf;
+                v = q == 0 ? hi : sf - hi;
+            }
+            const __bf16 b = (__bf16)v;
+            out[q] = *reinterpret_cast<const uint16_t *>(&b);
+        }
+        *reinterpret_cast<uint4 *>(Cop + e * 8) = *reinterpret_cast<const uint4 *>(out);
+    }
+    if (blockIdx.x == 0) {
+        __shared__ float a[256], b[256], r[256];
+        const int kpad = nchunks * 32;
+        float mn = 0.0f, ms = 0.0f, mr = 0.0f;
+        for (int c = threadIdx.x; c < k; c += 256) {
+            mn = fmaxf(mn, cn[c]);
+            ms = fmaxf(ms, csq[c]);
+            mr = fmaxf(mr, cn[kpad + c]);
+        }
+        a[threadIdx.x] = mn;
+        b[threadIdx.x] = ms;
+        r[threadIdx.x] = mr;
+        __syncthreads();
+        for (int h = 128; h > 0; h >>= 1) {
+            if ((int)threadIdx.x < h) {
+                a[threadIdx.x] = fmaxf(a[threadIdx.x], a[threadIdx.x + h]);
+                b[threadIdx.x] = fmaxf(b[threadIdx.x], b[threadIdx.x + h]);
+                r[threadIdx.x] = fmaxf(r[threadIdx.x], r[threadIdx.x + h]);
+            }
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) {
+            maxes[0] = a[0];
+            maxes[1] = b[0];
+            maxes[2] = r[0];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ the screen
+//
+// Window. For a row x and centre c, A_c = |c|^2 - 2 x.c and D_c = |x - c|^2 = |x|^2 + A_c (exact reals). The
+// matrix cores give a'_c = sum_j bf16(x_j) bf16(-2 c_j) + q_h + q_l (|c|^2 as two bf16 pieces). With the rounding
+// residuals e = bf16(x) - x and f_c = bf16(-2c) - (-2c) (their norms computed exactly per row and per centre and
+// rounded up), sum_j bf16(x_j) bf16(-2c_j) + 2 x.c = -2 e.c + x.f_c + e.f_c, so by Cauchy-Schwarz its size is at
+// most 2|e||c| + |x||f_c| + |e||f_c|. Products of bf16 values are exact in float32; the float32 accumulation of
+// NACC = DP + 2 terms adds at most gamma_NACC times their absolute sum (<= 2.04 |x||c| + 1.01 |c|^2); the
+// two-piece |c|^2 is off by at most 2^-16 relative. Hence, uniformly in c,
+//     |a'_c - A_c| <= E = (2|e| max|c| + |x| max|f| + |e| max|f|)(1 + 2^-20) + 2.04 gamma_NACC |x| max|c|
+//                         + GAM2 max|c|^2 + FLUSH (|x| + max|c|) + TINY,     GAM2 = 1.01 gamma_NACC + 2^-16 + 2^-23
+// (bf16 rounding to nearest has unit roundoff 2^-8, so |e| <= 2^-8 |x| and |f| <= 2^-7 |c|: E is never above the
+// plain worst case, and for typical data it is about 2.5 times smaller). The rows loop's float32 direct form s_c satisfies |s_c - D_c| <= g D_c (g = gamma_{D+2}), so a
+// centre can hold the minimum only if a'_c - a'_m <= 2E + 2 g/(1-g) D_m, with D_m <= |x|^2 + a'_m + E for the
+// screen minimiser m. Keys carry the centre index in their low IB mantissa bits (relative perturbation <= RHO),
+// absorbed by the test. Pass A finds the smallest key of each row; pass B recomputes the same screen values
+// (same operands, same instruction sequence, so the same bits) and lists every centre whose key is inside the
+// window. A half-row with more than KB_HALF such centres (or non-finite data) sends the row to a full scan.
+
+template <int DS>
+__global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
+    const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
+    const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
+    int approx, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
+    km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
+    constexpr int DP = 16 * DS, AK = DS + 1, NACC = DP + 2;
+    constexpr float GACC = (float)(2.04 * kb_gamma(NACC) * (1.0 + 0x1p-20));
+    constexpr float GAM2 = (float)((1.01 * kb_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
+    constexpr float FLUSH = (float)0x1p-119;
+    constexpr float TINY = (float)((DP + 2) * 0x1p-118);
+    if (stop && *stop) return;
+    extern __shared__ float lds[];
+    char *ring = reinterpret_cast<char *>(lds);   // two slices of at most KB_SLICE K-steps, 1 KB each
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int h = lane >> 5;
+    const int64_t ntiles = (n + 31) / 32;
+    const int64_t tile = (int64_t)blockIdx.x * KB_WAVES + wave;
+    const bool have = tile < ntiles;
+    const int64_t row = tile * 32 + (lane & 31);
+    const bool real_row = have && row < n;
+
+    // this wave's 32 rows as B operands (zeros past the last tile)
+    bf16x8 B[DS];
+#pragma unroll
+    for (int s = 0; s < DS; s++) {
+        if (have) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(X16T + ((tile * DS + s) * 64 + lane) * 8);
+            B[s] = *reinterpret_cast<const bf16x8 *>(&v);
+        } else {
+            B[s] = bf16x8{};
+        }
+    }
+    bf16x8 Bone;
+#pragma unroll
+    for (int q = 0; q < 8; q++) Bone[q] = (__bf16)((h == 0 && q < 2) ? 1.0f : 0.0f);
+    const uint32_t IMASK = (1u << ib) - 1u;
+
+    // A operand slices: chunk ch is SPC slices of SLK K-steps (the last possibly shorter), staged through a
+    // two-slice LDS ring; slice g (counted over both passes) is loaded while slice g - 1 is multiplied.
+    constexpr int SPC = (AK + KB_SLICE - 1) / KB_SLICE;
+    constexpr int SLK = (AK + SPC - 1) / SPC;
+    const int passes = approx ? 1 : 2;
+    const int GP = nchunks * SPC;
+    const int G = passes * GP;
+    auto issue = [&](int g) {
+        char *buf = ring + (g & 1) * (SLK * 1024);
+        const int gl = g % GP;
+        const int ch = gl / SPC, sl = gl - (gl / SPC) * SPC;
+        const int s0 = sl * SLK;
+        const int ns = (AK - s0) < SLK ? (AK - s0) : SLK;
+        for (int j = wave; j < ns; j += KB_WAVES) {
+            const uint16_t *src = Cop + (((int64_t)ch * AK + s0 + j) * 64 + lane) * 8;
+            __builtin_amdgcn_global_load_lds((gbl_vptr)src, (lds_vptr)(buf + j * 1024), 16, 0, 0);
+        }
+    };
+    // one chunk's screen values: acc element v is centre 32 ch + 8 (v / 4) + 4 h + v % 4 against this lane's row
+    auto screen_chunk = [&](int g0, f32x16 &acc) {
+        acc = f32x16{};
+#pragma unroll
+        for (int sl = 0; sl < SPC; sl++) {
+            const int g = g0 + sl;
+            const char *cur = ring + (g & 1) * (SLK * 1024);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (g + 1 < G) issue(g + 1);
+#pragma unroll
+            for (int j = 0; j < SLK; j++) {
+                const int s = sl * SLK + j;   // compile-time after unrolling
+                if (s < AK) {
+                    const bf16x8 A = *reinterpret_cast<const bf16x8 *>(cur + j * 1024 + lane * 16);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, s < DS ? B[s < DS ? s : 0] : Bone, acc, 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // ---- pass A: the smallest key of the row
+    issue(0);
+    float m1 = 3.4e38f;
+    for (int ch = 0; ch < nchunks; ch++) {
+        f32x16 acc;
+        screen_chunk(ch * SPC, acc);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
+            m1 = kb_min(m1, kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx));
+        }
+    }
+    m1 = kb_min(m1, kb_partner(m1, lane));   // both halves of the row
+    const float xsq_up = real_row ? xsq[2 * row] : 0.0f;
+    const float exn = real_row ? xsq[2 * row + 1] : 0.0f;
+    const bool finite = xsq_up < INFINITY && m1 < 3.0e38f;
+    // the window threshold and a key bound Tp with key <= Tp whenever key - rho |key| <= T
+    float T = -INFINITY, Tp = -INFINITY;
+    if (!approx && finite && real_row) {
+        const float cnmax = maxes[0], csqmax = maxes[1], fmax = maxes[2];
+        const float GDIR = (float)(kb_gamma(d + 2) / (1.0 - kb_gamma(d + 2)) * (1.0 + 0x1p-20));
+        const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
+        const float E = (2.0f * exn * cnmax + nx * fmax + exn * fmax) * (1.0f + 0x1p-20f) + GACC * nx * cnmax +
+                        GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
+        const float akm = m1 + rho * fabsf(m1);
+        const float dm_up = fmaxf(0.0f, xsq_up + akm + E) * (1.0f + 0x1p-20f);
+        T = akm + ((2.0f * E + 2.0f * GDIR * dm_up) * (1.0f + 0x1p-20f) + TINY);
+        T = T + 0x1p-22f * fabsf(T);
+        Tp = (T >= 0.0f ? T / (1.0f - rho) : T / (1.0f + rho));
+        Tp = Tp + 0x1p-21f * fabsf(Tp);
+        if (!(T < INFINITY)) Tp = -INFINITY;
+    }
+    // ---- pass B: every centre inside the window; each half-row lane lists at most KB_HALF (more: a full scan)
+    int cnt = 0;
+    bool spill = false;
+    if (!approx) {
+        for (int ch = 0; ch < nchunks; ch++) {
+            f32x16 acc;
+            screen_chunk(GP + ch * SPC, acc);
+            uint64_t any = 0;
+            uint64_t bal[16];
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
+                bal[v] = __ballot(kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx) <= Tp);
+                any |= bal[v];
+            }
+            if (any) {   // rare after the first few: some row of the wave has a centre of this chunk in its window
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    if ((bal[v] >> lane) & 1ull) {
+                        const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
+                        if (cnt < KB_HALF && real_row) cand[row * KB_CAP + h * KB_HALF + cnt] = (uint16_t)cidx;
+                        if (cnt >= KB_HALF) spill = true;
+                        cnt++;
+                    }
+                }
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (!real_row) return;
+    const int cnt_o = (int)kb_f32u(kb_partner(kb_u32f((uint32_t)cnt), lane));
+    const bool spill_o = cnt_o > KB_HALF;
+    if (h != 0) return;
+    int code;
+    if (!finite) {
+        code = KB_OVER;   // non-finite data: the rows loop decides
+    } else if (approx) {
+        cand[row * KB_CAP] = (uint16_t)(kb_u32(m1) & IMASK);
+        code = 1;
+    } else if (spill || spill_o || cnt + cnt_o == 0) {
+        code = KB_OVER;   // an empty window cannot happen for finite data (the minimiser is inside it)
+    } else {
+        code = cnt | (cnt_o << 8);
+    }
+    ncand[row] = (uint16_t)code;
+    if (code == KB_OVER) over[atomicAdd(&ctl->n_over, 1u)] = (uint32_t)row;
+}
+
+// ------------------------------------------------------------------ exact rescoring
+
+// Block (256 threads) per 64 consecutive rows. Each (row, candidate) pair is a work item, items ordered by row and
+// then by ascending candidate index (each row's thread sorts its own list); a thread takes one item per round.
+// 32 dims at a time, the block stages its rows and its items' centres in LDS (coalesced loads, stride 33 floats
+// so lanes on different rows or items read different banks), the next chunk's loads in flight in registers while
+// the current chunk is used; every item carries its running direct-form sum across the chunks, so the dims are
+// added in ascending order. Then one thread per row takes its items in order with a strict '<': the rows loop
+// restricted to the candidates. Rows marked KB_OVER are left to k_big_fullscan.
+static constexpr int KB_RR = 64;      // rows per rescoring block
+static constexpr int KB_RT = 256;     // threads (= items per round) per rescoring block
+static constexpr int KB_RCH = 32;     // dims per LDS chunk
+template <bool V4>
+__global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__ X, int64_t n, int d,
+                                                       const float *__restrict__ C, int k,
+                                                       const uint16_t *__restrict__ ncand,
+                                                       const uint16_t *__restrict__ cand,
+                                                       uint32_t *__restrict__ labels, float *__restrict__ best,
+                                                       const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    __shared__ float xs[KB_RR * (KB_RCH + 1)];
+    __shared__ float cs[KB_RT * (KB_RCH + 1)];
+    __shared__ uint16_t it_c[KB_RR * KB_CAP];
+    __shared__ uint8_t it_r[KB_RR * KB_CAP];
+    __shared__ float it_s[KB_RR * KB_CAP];
+    __shared__ int first[KB_RR + 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t r0 = (int64_t)blockIdx.x * KB_RR;
+    const int nr = (int)((n - r0) < KB_RR ? (n - r0) : KB_RR);
+    // item lists: thread r owns row r; an exclusive scan of the counts (wave 0) gives each row its slots
+    int code = KB_OVER, cntr = 0;
+    if (tid < KB_RR && tid < nr) {
+        code = ncand[r0 + tid];
+        cntr = code == KB_OVER ? 0 : (code & 255) + (code >> 8);
+    }
+    if (tid < 64) {
+        int incl = cntr;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off);
+            if (lane >= off) incl += v;
+        }
+        first[tid] = incl - cntr;
+        if (tid == 63) first[KB_RR] = incl;
+    }
+    __syncthreads();
+    if (tid < nr && cntr > 0) {
+        const int b = first[tid];
+        int m = b;
+        for (int half = 0; half < 2; half++) {
+            const int nc = half ? code >> 8 : code & 255;
+            for (int i = 0; i < nc; i++) {
+                const uint16_t v = cand[(r0 + tid) * KB_CAP + half * KB_HALF + i];
+                int j = m - 1;
+                while (j >= b && it_c[j] > v) { it_c[j + 1] = it_c[j]; j--; }
+                it_c[j + 1] = v;
+                it_r[m] = (uint8_t)tid;
+                m++;
+            }
+        }
+    }
+    __syncthreads();
+    const int items = first[KB_RR];
+    // staging: with V4 (dims a multiple of 4, rows 16-byte aligned) 8 consecutive lanes fetch one 32-float chunk
+    // as float4s - thread t takes float4 t % 8 of rows t / 8 + 32 u and of items t / 8 + 32 u; otherwise floats
+    constexpr int XPT = KB_RR * KB_RCH / KB_RT;   // x values staged per thread per chunk
+    constexpr int CPT = KB_RCH;                   // centre values staged per thread per chunk (KB_RT items)
+    for (int q0 = 0; q0 < items; q0 += KB_RT) {
+        const int ni = (items - q0) < KB_RT ? (items - q0) : KB_RT;
+        const int q = q0 + tid;
+        const int ir = q < items ? (int)it_r[q] : 0;
+        float sacc = 0.0f;
+        float xv[XPT], cv[CPT];
+        const float *cbase[CPT / 4];
+        if (V4) {
+#pragma unroll
+            for (int u = 0; u < CPT / 4; u++) {
+                const int i = tid / 8 + 32 * u;
+                cbase[u] = i < ni ? C + (int64_t)it_c[q0 + i] * d + 4 * (tid % 8) : nullptr;
+            }
+        }
+        auto fetch = [&](int j0) {
+            const int w = (d - j0) < KB_RCH ? (d - j0) : KB_RCH;
+            if (V4) {
+#pragma unroll
+                for (int u = 0; u < XPT / 4; u++) {
+                    const int r = tid / 8 + 32 * u, p = tid % 8;
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (r < nr && 4 * p < w) v = *reinterpret_cast<const float4 *>(X + (r0 + r) * d + j0 + 4 * p);
+                    xv[4 * u] = v.x;
+                    xv[4 * u + 1] = v.y;
+                    xv[4 * u + 2] = v.z;
+                    xv[4 * u + 3] = v.w;
+                }
+#pragma unroll
+                for (int u = 0; u < CPT / 4; u++) {
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (cbase[u] && 4 * (tid % 8) < w) v = *reinterpret_cast<const float4 *>(cbase[u] + j0);
+                    cv[4 * u] = v.x;
+                    cv[4 * u + 1] = v.y;
+                    cv[4 * u + 2] = v.z;
+                    cv[4 * u + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < XPT; u++) {
+                    const int e = tid + KB_RT * u;
+                    const int r = e / KB_RCH, jj = e % KB_RCH;
+                    xv[u] = (r < nr && jj < w) ? X[(r0 + r) * d + j0 + jj] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < CPT; u++) {
+                    const int e = tid + KB_RT * u;
+                    const int i = e / KB_RCH, jj = e % KB_RCH;
+                    cv[u] = (i < ni && jj < w) ? C[(int64_t)it_c[q0 + i] * d + j0 + jj] : 0.0f;
+                }
+            }
+        };
+        fetch(0);
+        for (int j0 = 0; j0 < d; j0 += KB_RCH) {
+            const int w = (d - j0) < KB_RCH ? (d - j0) : KB_RCH;
+            __syncthreads();
+            if (V4) {
+#pragma unroll
+                for (int u = 0; u < XPT; u++)
+                    xs[(tid / 8 + 32 * (u / 4)) * (KB_RCH + 1) + 4 * (tid % 8) + (u % 4)] = xv[u];
+#pragma unroll
+                for (int u = 0; u < CPT; u++)
+                    cs[(tid / 8 + 32 * (u / 4)) * (KB_RCH + 1) + 4 * (tid % 8) + (u % 4)] = cv[u];
+            } else {
+#pragma unroll
+                for (int u = 0; u < XPT; u++) {
+                    const int e = tid + KB_RT * u;
+                    xs[(e / KB_RCH) * (KB_RCH + 1) + e % KB_RCH] = xv[u];
+                }
+#pragma unroll
+                for (int u = 0; u < CPT; u++) {
+                    const int e = tid + KB_RT * u;
+                    cs[(e / KB_RCH) * (KB_RCH + 1) + e % KB_RCH] = cv[u];
+                }
+            }
+            __syncthreads();
+            if (j0 + KB_RCH < d) fetch(j0 + KB_RCH);
+            if (q < items) {
+                const float *xr = xs + ir * (KB_RCH + 1);
+                const float *cc = cs + tid * (KB_RCH + 1);
+                float sv = sacc;
+                for (int jj = 0; jj < w; jj++) {
+                    const float t = xr[jj] - cc[jj];
+                    sv = sv + t * t;
+                }
+                sacc = sv;
+            }
+        }
+        if (q < items) it_s[q] = sacc;
+    }
+    __syncthreads();
+    if (tid < nr && code != KB_OVER) {
+        float bst = INFINITY;
+        uint32_t bl = 0;
+        for (int q = first[tid]; q < first[tid] + cntr; q++) {
+            const float sq = it_s[q];
+            if (sq < bst) { bst = sq; bl = (uint32_t)it_c[q]; }
+        }
+        labels[r0 + tid] = bl;
+        best[r0 + tid] = bst;
+    }
+}
+
+// Block per listed row: the rows loop over every centre. The row sits in LDS; 256 centres at a time are staged
+// 32 dims per chunk (coalesced), thread t carrying the direct-form sum of centre c0 + t; each thread keeps its
+// smallest value over its centres (ascending, strict '<'), then the block keeps the smallest value, lowest index
+// among equal values - the rows loop's label and best.
+__global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ X, int d, const float *__restrict__ C,
+                                                      int k, const uint32_t *__restrict__ over,
+                                                      km_control *__restrict__ ctl, uint32_t *__restrict__ labels,
+                                                      float *__restrict__ best, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ float xrow[];
+    __shared__ float cs[256 * (KB_RCH + 1)];
+    __shared__ float sb[256];
+    __shared__ uint32_t sl[256];
+    const int tid = threadIdx.x;
+    const uint32_t total = ctl->n_over;
+    if (blockIdx.x == 0 && tid == 0) atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)total);
+    for (uint32_t q = blockIdx.x; q < total; q += gridDim.x) {
+        const int64_t row = over[q];
+        __syncthreads();
+        for (int j = tid; j < d; j += 256) xrow[j] = X[row * d + j];
+        float bst = INFINITY;
+        uint32_t bl = 0;
+        for (int c0 = 0; c0 < k; c0 += 256) {
+            const int nc = (k - c0) < 256 ? (k - c0) : 256;
+            float sacc = 0.0f;
+            for (int j0 = 0; j0 < d; j0 += KB_RCH) {
+                const int w = (d - j0) < KB_RCH ? (d - j0) : KB_RCH;
+                __syncthreads();
+                for (int e = tid; e < nc * KB_RCH; e += 256) {
+                    const int i = e / KB_RCH, jj = e - (e / KB_RCH) * KB_RCH;
+                    cs[i * (KB_RCH + 1) + jj] = jj < w ? C[(int64_t)(c0 + i) * d + j0 + jj] : 0.0f;
+                }
+                __syncthreads();
+                if (tid < nc) {
+                    const float *cc = cs + tid * (KB_RCH + 1);
+                    float sv = sacc;
+                    for (int jj = 0; jj < w; jj++) {
+                        const float t = xrow[j0 + jj] - cc[jj];
+                        sv = sv + t * t;
+                    }
+                    sacc = sv;
+                }
+            }
+            if (tid < nc && sacc < bst) { bst = sacc; bl = (uint32_t)(c0 + tid); }
+        }
+        __syncthreads();
+        sb[tid] = bst;
+        sl[tid] = bl;
+        __syncthreads();
+        for (int hh = 128; hh > 0; hh >>= 1) {
+            if (tid < hh) {
+                const float ob = sb[tid + hh];
+                const uint32_t ol = sl[tid + hh];
+                if (ob < sb[tid] || (ob == sb[tid] && ol < sl[tid])) {
+                    sb[tid] = ob;
+                    sl[tid] = ol;
+                }
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            labels[row] = sl[0];
+            best[row] = sb[0];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ sorted accumulation
+//
+// A stable counting sort of the rows by label: per 4096-row block a histogram (LDS integer adds, exact), per
+// label an exclusive prefix over blocks on top of the labels before it, then each block places its rows in
+// ascending row order (rank among earlier rows of the same label in the block). Each cluster then sums its
+// rows in that order - ascending row index - in float64: 16 waves take 16 fixed consecutive ranges of the
+// cluster's rows, lanes take dims, and the wave sums are added in wave order. Count, best sum and coordinate
+// sums land as one range sum per entry (tmp, S = 1 per slice), the format the finish reads.
+
+static constexpr int KB_RB = 4096;   // rows per histogram / scatter block
+
+__global__ __launch_bounds__(256) void k_big_hist(const uint32_t *__restrict__ labels, int64_t n, int k,
+                                                  uint32_t *__restrict__ H, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ uint32_t cnt[];
+    for (int c = threadIdx.x; c < k; c += 256) cnt[c] = 0;
+    __syncthreads();
+    const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
+    const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
+    for (int64_t r = r0 + threadIdx.x; r < r1; r += 256) atomicAdd(&cnt[labels[r]], 1u);
+    __syncthreads();
+    for (int c = threadIdx.x; c < k; c += 256) H[(int64_t)blockIdx.x * k + c] = cnt[c];
+}
+
+// One block: O[b][c] = (rows with label < c) + (rows with label c in blocks before b); counts[c] = its total.
+__global__ __launch_bounds__(1024) void k_big_scan(uint32_t *__restrict__ H, int nb, int k,
+                                                   uint32_t *__restrict__ counts, uint32_t *__restrict__ base,
+                                                   const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    __shared__ uint32_t part[1024];
+    // per label: exclusive prefix over blocks, in place (16 loads in flight before their stores)
+    for (int c = threadIdx.x; c < k; c += 1024) {
+        uint32_t run = 0;
+        for (int b0 = 0; b0 < nb; b0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = b0 + u < nb ? H[(int64_t)(b0 + u) * k + c] : 0u;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (b0 + u < nb) {
+                    H[(int64_t)(b0 + u) * k + c] = run;
+                    run += v[u];
+                }
+        }
+        counts[c] = run;
+    }
+    __syncthreads();
+    // exclusive prefix over labels: each thread a contiguous range, then the range totals
+    const int per = (k + 1023) / 1024;
+    const int c0 = threadIdx.x * per, c1 = (c0 + per < k) ? c0 + per : k;
+    uint32_t s = 0;
+    for (int c = c0; c < c1; c++) s += counts[c];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t run = 0;
+        for (int t = 0; t < 1024; t++) {
+            const uint32_t v = part[t];
+            part[t] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    uint32_t run = part[threadIdx.x];
+    for (int c = c0; c < c1; c++) {
+        base[c] = run;
+        run += counts[c];
+    }
+}
+
+// Block per 4096 rows, 256 at a time: a row's place is base[label] + O[b][label] + (rows of its label earlier
+// in this block).
+__global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict__ labels, int64_t n, int k,
+                                                     const uint32_t *__restrict__ O, const uint32_t *__restrict__ base,
+                                                     uint32_t *__restrict__ perm, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ uint32_t run[];   // k running offsets, then 256 labels
+    uint32_t *lab = run + k;
+    for (int c = threadIdx.x; c < k; c += 256) run[c] = base[c] + O[(int64_t)blockIdx.x * k + c];
+    const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
+    const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
+    for (int64_t q = r0; q < r1; q += 256) {
+        const int64_t r = q + threadIdx.x;
+        const bool valid = r < r1;
+        const uint32_t L = valid ? labels[r] : 0xffffffffu;
+        __syncthreads();
+        lab[threadIdx.x] = L;
+        __syncthreads();
+        uint32_t before = 0, after = 0;
+        for (int t = 0; t < 256; t++) {
+            const uint32_t o = lab[t];
+            before += (t < (int)threadIdx.x && o == L) ? 1u : 0u;
+            after += (t > (int)threadIdx.x && o == L) ? 1u : 0u;
+        }
+        if (valid) perm[run[L] + before] = (uint32_t)r;
+        __syncthreads();
+        if (valid && after == 0) run[L] += before + 1;   // the last row of each label advances its offset
+    }
+}
+
+// Block per cluster (KB_SEGW waves, each a fixed consecutive range of the cluster's rows): entries [count, best, x_0 .. x_{d-1}] as float64 sums over the cluster's rows
+// in ascending row order, written to tmp[c * (d + 2) + e].
+static constexpr int KB_SEGW = 8;
+__global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__restrict__ X, int d, const float *__restrict__ best,
+                                                     const uint32_t *__restrict__ perm, int64_t r0,
+                                                     const uint32_t *__restrict__ counts,
+                                                     const uint32_t *__restrict__ base, int k,
+                                                     double *__restrict__ tmp, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ double part[];   // KB_SEGW waves x (d + 1)
+    const int c = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t cnt = counts[c], b0 = base[c];
+    const uint32_t q0 = b0 + (uint32_t)((uint64_t)cnt * wave / KB_SEGW);
+    const uint32_t q1 = b0 + (uint32_t)((uint64_t)cnt * (wave + 1) / KB_SEGW);
+    const int W = d + 2;
+    double *mine = part + (size_t)wave * (d + 1);
+    // lane owns dims lane, lane + 64, ...; dim d (the best column) is kept by lane d % 64 as the extra slot
+    constexpr int MAXJ = 13;   // dims per lane: ceil(769 / 64)
+    double acc[MAXJ];
+#pragma unroll
+    for (int i = 0; i < MAXJ; i++) acc[i] = 0.0;
+    // rows in order; the row indices of the next 8 are loaded ahead, and each row's values are loaded before
+    // they are added
+    uint32_t pf[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) pf[u] = q0 + u < q1 ? perm[q0 + u] : 0u;
+    for (uint32_t q = q0; q < q1; q += 8) {
+        uint32_t cur[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) cur[u] = pf[u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pf[u] = q + 8 + u < q1 ? perm[q + 8 + u] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (q + u < q1) {
+                const int64_t r = r0 + cur[u];
+                const float *x = X + r * d;
+                float v[MAXJ];
+#pragma unroll
+                for (int i = 0; i < MAXJ; i++) {
+                    const int j = lane + 64 * i;
+                    v[i] = j < d ? x[j] : (j == d ? best[r] : 0.0f);
+                }
+#pragma unroll
+                for (int i = 0; i < MAXJ; i++) acc[i] += (double)v[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXJ; i++) {
+        const int j = lane + 64 * i;
+        if (j <= d) mine[j] = acc[i];
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j <= d; j += 64 * KB_SEGW) {
+        double t = 0.0;
+        for (int w = 0; w < KB_SEGW; w++) t += part[(size_t)w * (d + 1) + j];
+        // column order [count, best, x...]
+        if (j < d) tmp[(int64_t)c * W + 2 + j] = t;
+        else tmp[(int64_t)c * W + 1] = t;
+    }
+    if (threadIdx.x == 0) tmp[(int64_t)c * W] = (double)cnt;
+}
+
+// ------------------------------------------------------------------ planning and launch
+
+typedef void (*screen_fn)(const uint16_t *, const float *, int64_t, int, const uint16_t *, const float *, int, int,
+                          int, float, int, uint16_t *, uint16_t *, uint32_t *, km_control *, const int32_t *);
+
+static screen_fn kb_screen_for(int DS) {
+    switch (DS) {
+        case 2: return k_big_screen<2>;
+        case 4: return k_big_screen<4>;
+        case 8: return k_big_screen<8>;
+        case 16: return k_big_screen<16>;
+        case 24: return k_big_screen<24>;
+        case 32: return k_big_screen<32>;
+        case 48: return k_big_screen<48>;
+        default: return nullptr;
+    }
+}
+
+static int kb_ds(int d) {
+    const int s = (d + 15) / 16;
+    const int opts[] = {2, 4, 8, 16, 24, 32, 48};
+    for (int o : opts)
+        if (s <= o) return o;
+    return 0;
+}
+
+km_big_plan km_plan_big(int64_t n, int d, int k) {
+    km_big_plan pl{};
+    if (d <= 16 || d > 768 || k < 1 || k > 4096 || n < 1) return pl;
+    pl.ok = 1;
+    pl.DS = kb_ds(d);
+    pl.kpad = (k + 31) / 32 * 32;
+    pl.nchunks = pl.kpad / 32;
+    int ib = 0;
+    while ((1 << ib) < pl.kpad) ib++;
+    if (ib < 1) ib = 1;
+    pl.ib = ib;
+    pl.ntiles = (n + 31) / 32;
+    pl.nb = (int)((n + KB_RB - 1) / KB_RB);
+    return pl;
+}
+
+size_t km_big_x16_elems(const km_big_plan &pl) { return (size_t)pl.ntiles * pl.DS * 64 * 8; }
+size_t km_big_cop_elems(const km_big_plan &pl) { return (size_t)pl.nchunks * (pl.DS + 1) * 64 * 8; }
+
+hipError_t km_launch_big_rows(const km_big_plan &pl, const float *X, int64_t n, int d, uint16_t *X16T, float *xsq,
+                              hipStream_t s) {
+    const int64_t threads = pl.ntiles * pl.DS * 64;
+    hipLaunchKernelGGL(k_big_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, X, n, d, pl.DS, X16T,
+                       pl.ntiles);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_xsq, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, X, n, d, xsq);
+    return hipGetLastError();
+}
+
+hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, int d, float *csq, float *cn,
+                                 uint16_t *Cop, float *maxes, km_control *ctl, const int32_t *stop, hipStream_t s) {
+    hipLaunchKernelGGL(k_big_cnorm, dim3((unsigned)((pl.kpad + 3) / 4)), dim3(256), 0, s, C, k, pl.kpad, d, csq, cn,
+                       ctl, stop);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t threads = (int64_t)pl.nchunks * (pl.DS + 1) * 64;
+    hipLaunchKernelGGL(k_big_centres, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, C, k, d, pl.DS,
+                       pl.nchunks, csq, cn, Cop, maxes, stop);
+    return hipGetLastError();
+}
+
+hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
+                                int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
+                                uint32_t *over, km_control *ctl, const int32_t *stop, hipStream_t s) {
+    screen_fn fn = kb_screen_for(pl.DS);
+    if (!fn) return hipErrorInvalidValue;
+    const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
+    const unsigned blocks = (unsigned)((pl.ntiles + KB_WAVES - 1) / KB_WAVES);
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), 2 * KB_SLICE * 1024, s, X16T, xsq, n, d, Cop, maxes, k,
+                       pl.nchunks, pl.ib, rho, mode == KM_APPROX ? 1 : 0, ncand, cand, over, ctl, stop);
+    return hipGetLastError();
+}
+
+hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
+                                 const uint16_t *cand, const uint32_t *over, km_control *ctl, uint32_t *labels,
+                                 float *best, const int32_t *stop, hipStream_t s) {
+    const bool v4 = (d % 4 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)C % 16 == 0);
+    hipLaunchKernelGGL(v4 ? k_big_rescore<true> : k_big_rescore<false>, dim3((unsigned)((n + KB_RR - 1) / KB_RR)),
+                       dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand, labels, best, stop);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), (size_t)d * 4, s, X, d, C, k, over, ctl, labels, best,
+                       stop);
+    return hipGetLastError();
+}
+
+hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
+                               const float *best, int k, uint32_t *H, uint32_t *counts, uint32_t *base,
+                               uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
+    hipLaunchKernelGGL(k_big_hist, dim3(pl.nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_scan, dim3(1), dim3(1024), 0, s, H, pl.nb, k, counts, base, stop);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_scatter, dim3(pl.nb), dim3(256), (size_t)(k + 256) * 4, s, labels, n, k, H, base, perm,
+                       stop);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_segsum, dim3(k), dim3(64 * KB_SEGW), (size_t)KB_SEGW * (d + 1) * 8, s, X, d, best, perm,
+                       (int64_t)0, counts, base, k, tmp, stop);
+    return hipGetLastError();
+}

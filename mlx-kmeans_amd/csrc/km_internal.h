@@ -12,7 +12,8 @@ struct km_control {
     int32_t need_reloc;  // the last completed pass left clusters empty while some row had best > 0
     int32_t n_empty;     // empty clusters in the last completed pass
     int32_t big;         // first index of the largest count in the last completed pass
-    int32_t pad0, pad1;
+    uint32_t n_over;     // rows the wide-row screen listed for a full scan in the running pass
+    int32_t pad1;
     double inertia;      // inertia of the last completed pass (of its input centres)
     double prev;         // inertia of the pass before it
     double tol;
@@ -28,6 +29,10 @@ enum km_kernel_id {
     KK_NORMALISE,
     KK_FUSED_ROWS,
     KK_FUSED_MFMA,
+    KK_BIG_PREP,
+    KK_BIG_SCREEN,
+    KK_BIG_RESCORE,
+    KK_BIG_ACCUM,
     KK_COUNT
 };
 extern const char *const km_kernel_names[KK_COUNT];
@@ -88,3 +93,31 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned);
 hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int d, const float *C, int k,
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s);
+
+// Wide rows (16 < dims <= 768, k <= 4096): bf16 MFMA screen keeping 8 keys per row, exact rescoring of the
+// candidates, stable counting sort by label and per-cluster float64 sums.
+struct km_big_plan {
+    int ok;
+    int DS;          // MFMA K-steps over the padded dims (16 DS >= dims)
+    int kpad;        // centres padded to a multiple of 32
+    int nchunks;     // kpad / 32
+    int ib;          // centre-index bits packed into keys
+    int64_t ntiles;  // 32-row tiles
+    int nb;          // 4096-row blocks of the sort
+};
+km_big_plan km_plan_big(int64_t n, int d, int k);
+size_t km_big_x16_elems(const km_big_plan &pl);   // uint16 elements of the bf16 row operands
+size_t km_big_cop_elems(const km_big_plan &pl);   // uint16 elements of the bf16 centre operands
+hipError_t km_launch_big_rows(const km_big_plan &pl, const float *X, int64_t n, int d, uint16_t *X16T, float *xsq,
+                              hipStream_t s);
+hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, int d, float *csq, float *cn,
+                                 uint16_t *Cop, float *maxes, km_control *ctl, const int32_t *stop, hipStream_t s);
+hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
+                                int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
+                                uint32_t *over, km_control *ctl, const int32_t *stop, hipStream_t s);
+hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
+                                 const uint16_t *cand, const uint32_t *over, km_control *ctl, uint32_t *labels,
+                                 float *best, const int32_t *stop, hipStream_t s);
+hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
+                               const float *best, int k, uint32_t *H, uint32_t *counts, uint32_t *base,
+                               uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s);

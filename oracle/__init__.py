@@ -51,6 +51,8 @@ def lib():
         L.orc_totals.restype = None
         L.orc_update.argtypes = [f64p, ctypes.c_int, ctypes.c_int, f32p, i64, u32p, f32p, f32p, f32p, f64p, i32p]
         L.orc_update.restype = None
+        L.orc_label_dist.argtypes = [f32p, i64, ctypes.c_int, f32p, u32p, f32p]
+        L.orc_label_dist.restype = None
         L.orc_cpu_pass.argtypes = [f32p, i64, ctypes.c_int, f32p, ctypes.c_int, ctypes.c_int, f64p]
         L.orc_cpu_pass.restype = ctypes.c_int
         _lib = L
@@ -79,6 +81,19 @@ def assign(X, C, variant=VARIANT_A1, nthreads=None):
     lib().orc_assign(_p(X, ctypes.c_float), n, d, _p(C, ctypes.c_float), k, variant,
                      nthreads or default_threads(), _p(labels, ctypes.c_uint32), _p(best, ctypes.c_float))
     return labels, best
+
+
+def distances_to(X, C, labels):
+    """The rows-loop float32 distance of every row to the centre its label names (core.py:851-856)."""
+    X, C = _f32(X), _f32(C)
+    n, d = X.shape
+    labels = np.ascontiguousarray(labels, dtype=np.uint32)
+    if len(labels) != n or (n and int(labels.max()) >= C.shape[0]):
+        raise ValueError("one label per row, each naming a centre")
+    out = np.empty(n, np.float32)
+    lib().orc_label_dist(_p(X, ctypes.c_float), n, d, _p(C, ctypes.c_float), _p(labels, ctypes.c_uint32),
+                         _p(out, ctypes.c_float))
+    return out
 
 
 def totals(X, labels, best, k):

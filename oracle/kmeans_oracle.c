@@ -22,6 +22,9 @@
  *                  ties, paired with ascending empty ids; the order tests/accuracy.py:115-116 states); each
  *                  relocated row leaves its old cluster; centres = sums/counts rounded to float32; clusters
  *                  still empty take the largest cluster's centre (np.argmax: first maximum).
+ *   orc_label_dist the direct-form distance of each row to a given label, the reference's kmeans_label_dist
+ *                  (core.py:851-856), which the approximate path uses for best (core.py:1061-1088): the same
+ *                  rows-loop arithmetic for one centre.
  *   orc_cpu_pass   the reference's native CPU backend, kmeans.mm:222-277 (cpu_block / assign_cpu): jobs of
  *                  CPU_BLOCK rows, each job a private float accumulator (count, best, x) on its own stack, the
  *                  job buffers reduced in double in job order. Threads replace GCD's dispatch_apply.
@@ -95,6 +98,11 @@ void orc_assign(const float *X, int64_t n, int d, const float *C, int k, int var
     for (int t = 1; t < used; t++) pthread_create(&th[t], NULL, assign_worker, &jobs[t]);
     if (used > 0) assign_worker(&jobs[0]);
     for (int t = 1; t < used; t++) pthread_join(th[t], NULL);
+}
+
+/* out[i] = the rows-loop distance of row i to centre labels[i] (core.py:851-856). */
+void orc_label_dist(const float *X, int64_t n, int d, const float *C, const uint32_t *labels, float *out) {
+    for (int64_t i = 0; i < n; i++) out[i] = dist_variant(X + (size_t)i * d, C + (size_t)labels[i] * d, d, 0);
 }
 
 /* tot is (k, d+2) doubles: [count, sum best, sum x_0 .. sum x_{d-1}], summed in long double in row order. */

@@ -33,7 +33,9 @@ def lib():
 
 
 def mfma_served(d, k):
-    return d in (16, 32) and k <= 64 or d == 64 and k <= 32
+    """The fused screen serves d = 16, 32 with k <= 64 and d = 64 with k <= 32; the wide-row screen serves
+    16 < d <= 768 with k <= 4096."""
+    return d in (16, 32) and k <= 64 or d == 64 and k <= 32 or 16 < d <= 768 and k <= 4096
 
 
 def fused_served(d, k):
@@ -131,7 +133,8 @@ def test_fit_loop_matches_oracle(lib, name):
 
 
 @pytest.mark.parametrize("d,k", [(32, 64), (16, 64), (32, 32), (64, 32), (16, 32), (32, 40), (16, 8), (12, 20),
-                                 (8, 8), (5, 33), (4, 12), (3, 7), (2, 64), (1, 5)])
+                                 (8, 8), (5, 33), (4, 12), (3, 7), (2, 64), (1, 5), (48, 100), (96, 33), (200, 64),
+                                 (17, 5), (768, 40), (33, 300)])
 def test_paths_are_bit_identical(lib, d, k):
     """Every path that serves a shape returns the rows path's labels and best bit for bit and the same counts;
     sums agree to the accumulation tolerance. 60,011 rows: a ragged tail for every block size."""
@@ -251,6 +254,65 @@ def test_lowd_workloads_full_size(lib, name):
     assert ctx.last_path() == "fused"
     rng = np.random.default_rng(2)
     idx = np.sort(rng.choice(n, 200_000, replace=False))
+    ol, ob = oracle.assign(X[idx], C0)
+    assert np.array_equal(labels[idx], ol)
+    assert np.array_equal(best[idx].view(np.uint32), ob.view(np.uint32))
+    counts = np.rint(tot[:, 0]).astype(np.int64)
+    assert int(counts.sum()) == n
+    assert np.array_equal(counts, np.bincount(labels, minlength=k))
+    colsum = X.astype(np.float64).sum(0)
+    assert np.max(np.abs(tot[:, 2:].sum(0) - colsum)) <= 1e-6 * np.abs(X).astype(np.float64).sum(0).max()
+    bsum = np.bincount(labels, weights=best.astype(np.float64), minlength=k)
+    np.testing.assert_allclose(tot[:, 1], bsum, rtol=1e-6)
+    tot2, labels2, _ = ctx.run_pass(C0, labels=True)
+    assert np.array_equal(tot, tot2) and np.array_equal(labels, labels2)
+    ctx.close()
+
+
+def test_approx_mode_properties(lib):
+    """exact=False on wide rows (the reference's approximate path, core.py:1061-1088): labels come from the bf16
+    screen's minimiser, best is the exact float32 direct-form distance to that label (bit-identical to the oracle's
+    distance for the same label), so every row's best is >= its exact best and the inertia >= the exact inertia;
+    labels agree with exact mode on nearly every row (the reference allows 10% disagreement, tests/reuse.py:61)."""
+    import oracle
+    rng = np.random.default_rng(11)
+    n, d, k = 30_000, 256, 128
+    cen = rng.standard_normal((k, d)).astype(np.float32)
+    X = (cen[rng.integers(0, k, n)] + 0.3 * rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(n, k, replace=False)]
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say("[gpu] approx mode")
+    te, le, be = ctx.run_pass(C, mode=lib.KM_EXACT, labels=True, best=True)
+    ta, la, ba = ctx.run_pass(C, mode=lib.KM_APPROX, labels=True, best=True)
+    assert ctx.last_path() == "mfma"
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(le, ol) and np.array_equal(be.view(np.uint32), ob.view(np.uint32))
+    db = oracle.distances_to(X, C, la)
+    assert np.array_equal(ba.view(np.uint32), db.view(np.uint32))
+    assert np.all(ba >= be)
+    assert float(ta[:, 1].sum()) >= float(te[:, 1].sum())
+    assert np.mean(la != le) <= 0.10
+    assert int(np.rint(ta[:, 0]).sum()) == n
+    ctx.close()
+
+
+def test_embed_workload_full_size(lib):
+    """1M x 768, k=1024 at full size on the wide-row screen: labels and best of a 3000-row sample bit-identical to
+    the oracle's; counts sum to n and match the labels; per-cluster sums add up to the column sums of X; a rerun
+    gives the same bits."""
+    import oracle
+    from mlx_kmeans import synthetic
+    w = synthetic.embed_d768()
+    X, C0, k = w["X"], w["C0"], w["k"]
+    n = len(X)
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] embed full size n={n}")
+    tot, labels, best = ctx.run_pass(C0, labels=True, best=True)
+    assert ctx.last_path() == "mfma"
+    rng = np.random.default_rng(3)
+    idx = np.sort(rng.choice(n, 3000, replace=False))
     ol, ob = oracle.assign(X[idx], C0)
     assert np.array_equal(labels[idx], ol)
     assert np.array_equal(best[idx].view(np.uint32), ob.view(np.uint32))

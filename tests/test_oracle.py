@@ -199,3 +199,21 @@ def test_a1_and_fma_variants_differ_only_at_ties(oracle):
     _, ref_d = oracle.reference_f64(X, C)
     assert oracle.label_tolerance(X, C, lf, ref_d) == 0
     assert flips < len(X) * 0.01
+
+
+def test_label_distances_pinned(oracle):
+    """distances_to (core.py:851-856) on integer-valued data, where every float32 step is exact: equal to the
+    integer squared distance to the given (arbitrary) labels; and equal bit for bit to assign's best for assign's
+    own labels on float data."""
+    rng = np.random.default_rng(4)
+    X = rng.integers(-50, 50, size=(3000, 24)).astype(np.float32)
+    C = rng.integers(-50, 50, size=(37, 24)).astype(np.float32)
+    lab = rng.integers(0, 37, size=3000).astype(np.uint32)
+    want = ((X.astype(np.int64) - C[lab].astype(np.int64)) ** 2).sum(1)
+    assert np.array_equal(oracle.distances_to(X, C, lab), want.astype(np.float32))
+    Xf = rng.standard_normal((4000, 40)).astype(np.float32)
+    Cf = Xf[rng.choice(4000, 50, replace=False)]
+    labels, best = oracle.assign(Xf, Cf)
+    assert np.array_equal(oracle.distances_to(Xf, Cf, labels).view(np.uint32), best.view(np.uint32))
+    with pytest.raises(ValueError):
+        oracle.distances_to(Xf, Cf, np.full(4000, 50, np.uint32))
