@@ -453,6 +453,8 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
     if (fam == FAM_BIG) return run_big(c, k, mode, labels_d, best_d, stop, pass, tol, flags);
 
     if (fam == FAM_MFMA_FUSED) {
+        // without per-row outputs the kernel skips the direct form for rows the screen settles alone
+        const int want_best = (labels_d || best_d) ? 1 : 0;
         size_t total_rb = 0;
         std::vector<km_mfma_plan> plans;
         for (auto &p : c->parts) {
@@ -468,8 +470,8 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
             float *bst = best_d ? best_d + row0 : nullptr;
             HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
-                return km_launch_mfma(plans[i], 1, p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p, rb,
-                                      c->ctl, stop, c->stream);
+                return km_launch_mfma(plans[i], want_best, p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p,
+                                      rb, c->ctl, stop, c->stream);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;

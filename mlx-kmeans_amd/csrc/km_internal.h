@@ -78,7 +78,9 @@ struct km_mfma_plan {
     size_t lds;
 };
 km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused);
-hipError_t km_launch_mfma(const km_mfma_plan &pl, int fused, const float *X, int64_t n, int d, const float *C,
+// want_best: every row's exact direct-form distance (labels/best outputs); without it, rows the screen settles
+// alone add an FMA-form distance to the pass inertia (their labels are exact either way).
+hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
                           const int32_t *stop, hipStream_t s);
 

@@ -17,8 +17,11 @@
 // Accumulation (ACCUM), also on the matrix cores: per 64-row block, sums (centres x dims) += onehot^T (centres x
 // rows) x rows. The one-hot operand is exact in bf16 (0 or 1); each row value is split exactly into three bf16
 // pieces (split3), so the float32 MFMA accumulators add the float32 row values themselves, rounded only by the
-// accumulation. Counts are integer-exact counts of the rows that did not match each centre; the inertia is a
-// per-lane Kahan sum. At the end of its rows each wave leaves its accumulators in LDS and the block folds them
+// accumulation. Counts are LDS integer adds (exact, order-free). The block's inertia partial is a per-lane Kahan sum
+// of the rows' distances. With BEST every row's distance is the exact direct form (labels, best outputs); without
+// it only rows whose window holds several centres are rescored with the direct form, and the others - whose label
+// is the screen's minimiser, exactly the rows loop's label - add their distance in FMA form, which agrees with the
+// direct form to float32 rounding. At the end of its rows each wave leaves its accumulators in LDS and the block folds them
 // in wave order (Neumaier across waves) into one partial per block; the partials are reduced in a fixed order
 // in float64 by a separate kernel. Every step has a fixed order, so the result is the same on every run.
 #pragma clang fp contract(off)
@@ -86,7 +89,8 @@ struct Geo {
     static constexpr int AK = 2 * DS + 1;           // A-operand K-steps: high pieces, low pieces, |c|^2
     static constexpr int KT = KP / 32;              // centre tiles
     static constexpr int IB = KT <= 1 ? 4 : KT <= 2 ? 5 : 6;   // index bits packed into keys (16 KT values)
-    static constexpr int CS = D + 4;                // LDS row stride of the float32 centres
+    static constexpr int CS = D + 1;                // LDS row stride of the float32 centres (odd: lanes reading
+                                                    // different centres' rows hit different banks)
     static constexpr int AS = D + 1;                // LDS row stride of the accumulators
 };
 
@@ -245,7 +249,7 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
     return *reinterpret_cast<const float *>(buf + (tile * L::QI + q) * L::RB + slot * 16 + (dim & 3) * 4);
 }
 
-template <int D, int KP, int WAVES, bool ACCUM>
+template <int D, int KP, int WAVES, bool ACCUM, bool BEST>
 __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k, int64_t rbs,
     uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
@@ -255,8 +259,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     constexpr int DH = G::DH, DS = G::DS, KT = G::KT, CS = G::CS, W = D + 2;
     constexpr int NT = (D + 31) / 32;                 // 32-dim tiles of the accumulation
     constexpr int FOLD = (KP * 32 * NT + 2 * KP) * 4; // bytes of the end-of-block fold per wave
-    // per wave: two block buffers + 64 uint16 labels during the loop, the fold after it
-    constexpr int WBYTES = (2 * L::BUF + 128 > FOLD) ? 2 * L::BUF + 128 : FOLD;
+    // per wave: two block buffers, 64 uint16 labels and KP uint32 counts during the loop, the fold after it
+    constexpr int LOOPB = 2 * L::BUF + 128 + 4 * KP;
+    constexpr int WBYTES = (LOOPB > FOLD + 4 * KP) ? LOOPB : FOLD + 4 * KP;
     // window constants
     constexpr int NACC = 2 * G::DP + 2;
     constexpr float BETA = (float)((2.0 * (0x1p-8 + 0x1p-16 + 0x1p-24) + 2.04 * km_gamma(NACC)) * (1.0 + 0x1p-20));
@@ -276,6 +281,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     char *wbase = reinterpret_cast<char *>(lds + KP * CS) + wave * WBYTES;
     uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * L::BUF);   // labels of the block (0x4000: no row)
+    uint32_t *CNT = reinterpret_cast<uint32_t *>(wbase + WBYTES - 4 * KP);   // rows per centre (this wave)
 
     const int64_t r_begin = (int64_t)blockIdx.x * rbs;
     const int64_t r_end = (r_begin + rbs < n) ? r_begin + rbs : n;
@@ -341,10 +347,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     for (int t = 0; t < KT; t++)
 #pragma unroll
         for (int u = 0; u < NT; u++) sacc[t][u] = f32x16{};
-    uint32_t nomatch[KT];     // rows compared by this lane whose label is not centre 32t + ln
-#pragma unroll
-    for (int t = 0; t < KT; t++) nomatch[t] = 0;
-    uint32_t rows_seen = 0;   // rows this lane compared
+    for (int c = lane; c < KP; c += 64) CNT[c] = 0u;
     const uint32_t ones = 0x00010001u, c3f80 = 0x3f803f80u, cneg = 0xc080c080u;
 
     // the two block buffers alternate by offset (pointer arithmetic keeps the LDS address space visible)
@@ -445,56 +448,80 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                 }
             }
         }
-        // ---- every lane takes its whole row
-        float lo[DH], hi[DH];
-#pragma unroll
-        for (int q = 0; q < DH; q++) own_halves(xa[q], xb[q], lo[q], hi[q]);
-        // ---- exact rescoring: the lowest candidate, then (rare) the others in ascending order, strict '<'
-        int c0 = 0;
-        {
-            bool got = false;
-#pragma unroll
-            for (int t = 0; t < KT; t++)
-                if (!got && mw[t]) {
-                    c0 = 32 * t + __builtin_ctz(mw[t]);
-                    got = true;
-                }
-        }
-        float bst;
-        uint32_t bl = (uint32_t)c0;
-        {
-            const float *cc = Cl + c0 * CS;
-            float s = 0.0f;
-#pragma unroll
-            for (int q = 0; q < DH; q++) { const float t = lo[q] - cc[q]; s = s + t * t; }
-#pragma unroll
-            for (int q = 0; q < DH; q++) { const float t = hi[q] - cc[DH + q]; s = s + t * t; }
-            bst = s;
-            // the rows loop keeps best = INFINITY and label 0 when no distance compares below it (NaN)
-            if (!(s < INFINITY)) { bst = INFINITY; bl = 0; }
-        }
-        if (!unique) {
+        float bst = 0.0f;
+        uint32_t bl = unique ? (uint32_t)cm : 0u;
+        if (BEST || __ballot(!unique && valid) != 0) {
             asm volatile("" ::: "memory");
-            mw[c0 >> 5] &= ~(1u << (c0 & 31));
-            fallback += valid ? 1u : 0u;
+            // ---- every lane takes its whole row
+            float lo[DH], hi[DH];
 #pragma unroll
-            for (int t = 0; t < KT; t++) {
-                uint32_t wv = mw[t];
-                while (wv) {
-                    const int b = __builtin_ctz(wv);
-                    wv &= wv - 1u;
-                    const int c = 32 * t + b;
-                    const float *cc = Cl + c * CS;
+            for (int q = 0; q < DH; q++) own_halves(xa[q], xb[q], lo[q], hi[q]);
+            if (BEST || !unique) {
+                // ---- exact rescoring: the lowest candidate, then (rare) the others in ascending order, strict '<'
+                int c0 = 0;
+                {
+                    bool got = false;
+#pragma unroll
+                    for (int t = 0; t < KT; t++)
+                        if (!got && mw[t]) {
+                            c0 = 32 * t + __builtin_ctz(mw[t]);
+                            got = true;
+                        }
+                }
+                bl = (uint32_t)c0;
+                {
+                    const float *cc = Cl + c0 * CS;
                     float s = 0.0f;
-                    for (int q = 0; q < DH; q++) { const float tq = lo[q] - cc[q]; s = s + tq * tq; }
-                    for (int q = 0; q < DH; q++) { const float tq = hi[q] - cc[DH + q]; s = s + tq * tq; }
-                    if (s < bst) { bst = s; bl = (uint32_t)c; }
+#pragma unroll
+                    for (int q = 0; q < DH; q++) { const float t = lo[q] - cc[q]; s = s + t * t; }
+#pragma unroll
+                    for (int q = 0; q < DH; q++) { const float t = hi[q] - cc[DH + q]; s = s + t * t; }
+                    bst = s;
+                    // the rows loop keeps best = INFINITY and label 0 when no distance compares below it (NaN)
+                    if (!(s < INFINITY)) { bst = INFINITY; bl = 0; }
+                }
+                if (!unique) {
+                    asm volatile("" ::: "memory");
+                    mw[c0 >> 5] &= ~(1u << (c0 & 31));
+                    fallback += valid ? 1u : 0u;
+#pragma unroll
+                    for (int t = 0; t < KT; t++) {
+                        uint32_t wv = mw[t];
+                        while (wv) {
+                            const int b = __builtin_ctz(wv);
+                            wv &= wv - 1u;
+                            const int c = 32 * t + b;
+                            const float *cc = Cl + c * CS;
+                            float s = 0.0f;
+                            for (int q = 0; q < DH; q++) { const float tq = lo[q] - cc[q]; s = s + tq * tq; }
+                            for (int q = 0; q < DH; q++) { const float tq = hi[q] - cc[DH + q]; s = s + tq * tq; }
+                            if (s < bst) { bst = s; bl = (uint32_t)c; }
+                        }
+                    }
                 }
             }
         }
+        if (!BEST && ACCUM) {
+            // inertia of the rows the screen settled alone: |x - c_m|^2 in FMA form on the half-rows each lane
+            // holds (the label needs no distance; the sum agrees with the direct form's to float32 rounding)
+            const uint32_t cmo = unique ? (uint32_t)cm : 0u;
+            const auto sw = __builtin_amdgcn_permlane32_swap(cmo, cmo, false, false);
+            const uint32_t cA = lane < 32 ? cmo : sw[0], cB = lane < 32 ? sw[1] : cmo;
+            const float *ca = Cl + cA * CS + h * DH, *cbp = Cl + cB * CS + h * DH;
+            float pa[4] = {0.0f, 0.0f, 0.0f, 0.0f}, pb[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains each
+#pragma unroll
+            for (int q = 0; q < DH; q++) {
+                const float ta = xa[q] - ca[q], tb = xb[q] - cbp[q];
+                pa[q & 3] = __builtin_fmaf(ta, ta, pa[q & 3]);
+                pb[q & 3] = __builtin_fmaf(tb, tb, pb[q & 3]);
+            }
+            float s0h, s1h;
+            own_halves((pa[0] + pa[1]) + (pa[2] + pa[3]), (pb[0] + pb[1]) + (pb[2] + pb[3]), s0h, s1h);
+            if (unique) bst = s0h + s1h;
+        }
         if (valid) {
             if (labels) labels[row] = bl;
-            if (best) best[row] = bst;
+            if (BEST && best) best[row] = bst;
         }
         if (ACCUM) {
             // ---- accumulation on the matrix cores: sums (centres x dims) += onehot^T (centres x rows) x rows
@@ -504,13 +531,11 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                 ine_c = (tt - ine_s) - y;
                 ine_s = tt;
             }
+            if (valid) atomicAdd(&CNT[bl], 1u);   // integer adds: the order does not matter
             L16[lane] = valid ? (uint16_t)bl : (uint16_t)0x4000u;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            uint32_t miss[KT];   // per 16-bit half, at most 16 per block
-#pragma unroll
-            for (int t = 0; t < KT; t++) miss[t] = 0;
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 const int rbase = 16 * ks + 8 * h;           // this lane's 8 rows of the K-step
@@ -527,7 +552,6 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                         uint32_t y, oh;
                         asm("v_pk_min_u16 %0, %1, %2" : "=v"(y) : "v"(lab2[p] ^ mm), "v"(ones));
                         asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(oh) : "v"(y), "v"(cneg), "v"(c3f80));
-                        asm("v_pk_add_u16 %0, %1, %2" : "=v"(miss[t]) : "v"(miss[t]), "v"(y));
                         o[p] = oh;
                     }
                     OH[t] = *reinterpret_cast<bf16x8 *>(o);
@@ -548,9 +572,6 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                     }
                 }
             }
-            rows_seen += 32;
-#pragma unroll
-            for (int t = 0; t < KT; t++) nomatch[t] += (miss[t] & 0xffffu) + (miss[t] >> 16);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -580,7 +601,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         }
     }
     float *F = reinterpret_cast<float *>(wbase);                      // KP x (32 NT) sums of this wave
-    uint32_t *FC = reinterpret_cast<uint32_t *>(F + KP * 32 * NT);    // 2 x KP match counts (one per half)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int t = 0; t < KT; t++)
 #pragma unroll
@@ -590,9 +613,6 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                 const int c = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
                 F[c * (32 * NT) + 32 * u + ln] = sacc[t][u][v];
             }
-#pragma unroll
-    for (int t = 0; t < KT; t++)   // rows of this lane labelled 32t + ln
-        FC[h * KP + 32 * t + ln] = rows_seen - nomatch[t];
     __syncthreads();
     const int64_t kw = (int64_t)k * W;
     float *ps = psum + (int64_t)(rb0 + blockIdx.x) * kw;
@@ -603,10 +623,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         float s = 0.0f, cc = 0.0f;
         if (col == 0) {
             uint32_t tot = 0;
-            for (int w = 0; w < WAVES; w++) {
-                const uint32_t *fcw = reinterpret_cast<const uint32_t *>(base + w * WBYTES) + KP * 32 * NT;
-                tot += fcw[c] + fcw[KP + c];
-            }
+            for (int w = 0; w < WAVES; w++)
+                tot += reinterpret_cast<const uint32_t *>(base + w * WBYTES + WBYTES - 4 * KP)[c];
             s = (float)tot;
         } else if (col == 1) {
             if (c == 0) {
@@ -640,12 +658,12 @@ typedef void (*fused_fn)(const float *, int64_t, const float *, int, int64_t, ui
 // One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
 struct fused_entry {
     int d, kp;
-    fused_fn acc4, noacc4, acc2, noacc2;
+    fused_fn acc4, acc4b, acc2, acc2b;   // accumulating; "b": also the rows' exact distances (labels, best)
 };
 
-#define KM_FUSED(DD, KK)                                                                             \
-    {DD, KK, k_fused_mfma<DD, KK, 4, true>, k_fused_mfma<DD, KK, 4, false>, k_fused_mfma<DD, KK, 2, true>, \
-     k_fused_mfma<DD, KK, 2, false>}
+#define KM_FUSED(DD, KK)                                                                                     \
+    {DD, KK, k_fused_mfma<DD, KK, 4, true, false>, k_fused_mfma<DD, KK, 4, true, true>,                    \
+     k_fused_mfma<DD, KK, 2, true, false>, k_fused_mfma<DD, KK, 2, true, true>}
 
 static fused_entry g_fused[] = {
     KM_FUSED(16, 32), KM_FUSED(16, 64),
@@ -654,10 +672,11 @@ static fused_entry g_fused[] = {
 };
 #undef KM_FUSED
 
+// mirrors the kernel's layout: centres, then per wave max(two block buffers + labels + counts, fold + counts)
 static size_t lds_for(int d, int kp, int waves) {
-    const size_t loop = 2 * (size_t)(2 * (d / 8) * 1040) + 128;   // two block buffers + labels
-    const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float);
-    return (size_t)kp * (d + 4) * sizeof(float) + waves * (loop > fold ? loop : fold);
+    const size_t loop = 2 * (size_t)(2 * (d / 8) * 1040) + 128 + 4 * (size_t)kp;
+    const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float) + 4 * (size_t)kp;
+    return (size_t)kp * (d + 1) * sizeof(float) + waves * (loop > fold ? loop : fold);
 }
 
 static const fused_entry *find_fused(int d, int k) {
@@ -695,7 +714,7 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused) {
     fused_fn fn = waves == 4 ? fe->acc4 : fe->acc2;
     if (lds > 65536) {
         (void)hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        (void)hipFuncSetAttribute((const void *)(waves == 4 ? fe->noacc4 : fe->noacc2),
+        (void)hipFuncSetAttribute((const void *)(waves == 4 ? fe->acc4b : fe->acc2b),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
     int occ = 0;
@@ -718,12 +737,12 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused) {
     return pl;
 }
 
-hipError_t km_launch_mfma(const km_mfma_plan &pl, int fused, const float *X, int64_t n, int d, const float *C, int k,
-                          uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
+hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
+                          int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
                           const int32_t *stop, hipStream_t s) {
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
-    fused_fn fn = pl.waves == 4 ? (fused ? fe->acc4 : fe->noacc4) : (fused ? fe->acc2 : fe->noacc2);
+    fused_fn fn = pl.waves == 4 ? (want_best ? fe->acc4b : fe->acc4) : (want_best ? fe->acc2b : fe->acc2);
     hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, pl.rbs, labels, best, psum,
                        pcomp, rb0, ctl, stop);
     return hipGetLastError();
