@@ -17,8 +17,10 @@ class KMeans:
     iteration.
 
     accumulate is accepted for compatibility; every accumulation here is deterministic and compensated, so
-    "atomic" (the reference's non-reproducible option) is served by the deterministic path. exact=False is
-    accepted: the exact path is used (the reference also ignores the flag where the exact kernels are faster).
+    "atomic" (the reference's non-reproducible option) is served by the deterministic path. exact=False allows the
+    approximate assignment (estimator.py:18-30): where the wide-row path serves the shape, the label is the bf16
+    matrix-core screen's argmin taken on trust; elsewhere the exact kernels are also the fastest and run unchanged.
+    best and the sums are exact for the label chosen either way.
     algorithm="emeans" is not part of this engine.
 
     X may be anything array-like (numpy, pandas, lists of rows), a torch tensor (CUDA tensors are read in
@@ -43,6 +45,10 @@ class KMeans:
     @property
     def _method(self):
         return "auto" if self.exact else "approx"
+
+    @property
+    def _mode(self):
+        return core._mode(self._method)
 
     @classmethod
     def from_centers(cls, centers, **kwargs):
@@ -138,7 +144,7 @@ class KMeans:
                 C = self._normalise(C)
             prev = None
             for it in range(self.max_iter):
-                C, inertia, n_empty = data.ctx.lloyd_step(C)
+                C, inertia, n_empty = data.ctx.lloyd_step(C, mode=self._mode)
                 if not np.isfinite(inertia):
                     self._explain_nonfinite(data)
                 if self.spherical:
@@ -148,7 +154,8 @@ class KMeans:
                     break
                 prev = inertia
             return C, inertia, it + 1
-        C, inertia, iters, _ = data.ctx.fit(C, self.max_iter, self.tol, spherical=self.spherical)
+        C, inertia, iters, _ = data.ctx.fit(C, self.max_iter, self.tol, mode=self._mode,
+                                            spherical=self.spherical)
         if not np.isfinite(inertia):
             self._explain_nonfinite(data)
         return C, inertia, iters
@@ -166,7 +173,7 @@ class KMeans:
                 seed = None if self.random_state is None else self.random_state + run
                 C, inertia, iters = self._one_run(data, rows, seed)
                 # a Lloyd step reports the inertia before its update: score the final centres (estimator.py:199-204)
-                tot, labels, _ = data.ctx.run_pass(C, labels=True)
+                tot, labels, _ = data.ctx.run_pass(C, mode=self._mode, labels=True)
                 inertia = float(tot[:, 1].sum())
                 if not np.isfinite(inertia):
                     self._explain_nonfinite(data)
@@ -189,7 +196,7 @@ class KMeans:
                              f"{self.cluster_centers_.shape[1]}")
         data = parts if isinstance(parts, core.DeviceData) else core.DeviceData(parts)
         try:
-            tot, labels, _ = data.ctx.run_pass(self.cluster_centers_, labels=True)
+            tot, labels, _ = data.ctx.run_pass(self.cluster_centers_, mode=self._mode, labels=True)
             if not np.isfinite(tot[:, 1].sum()):
                 self._explain_nonfinite(data)
             return labels.astype(np.int64)

@@ -196,6 +196,27 @@ def test_estimator_known_answer_and_restarts():
         fitted.predict(np.zeros((3, 5), np.float32))
 
 
+def test_estimator_exact_and_approx():
+    """KMeans(exact=True) labels_ are the oracle's assignment to the returned centres, bit for bit, and inertia_ is
+    the oracle's inertia of those labels; KMeans(exact=False) (estimator.py:18-30) fits the same data to nearly the
+    same inertia (the reference quotes 0.003% more on GIST1M), and in both models predict(X) returns labels_."""
+    import oracle
+    from mlx_kmeans import KMeans
+    rng = np.random.default_rng(5)
+    n, d, k = 20_000, 256, 64
+    cen = (3.0 * rng.standard_normal((k, d))).astype(np.float32)
+    X = (cen[rng.integers(0, k, n)] + rng.standard_normal((n, d))).astype(np.float32)
+    say("[gpu] estimator exact vs approx")
+    ex = KMeans(n_clusters=k, max_iter=10, random_state=1).fit(X)
+    ol, ob = oracle.assign(X, ex.cluster_centers_)
+    assert np.array_equal(ex.labels_, ol.astype(np.int64))
+    assert abs(ex.inertia_ - float(ob.astype(np.float64).sum())) <= 1e-5 * ex.inertia_
+    ap = KMeans(n_clusters=k, max_iter=10, random_state=1, exact=False).fit(X)
+    assert ap.inertia_ <= ex.inertia_ * (1 + 1e-3)
+    for m in (ex, ap):
+        assert np.array_equal(m.predict(X), m.labels_)
+
+
 def test_estimator_nonfinite_is_explained():
     from mlx_kmeans import KMeans
     X = np.random.default_rng(0).standard_normal((1000, 4)).astype(np.float32)
