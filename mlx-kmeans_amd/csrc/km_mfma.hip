@@ -15,7 +15,8 @@
 // Accumulator element v (0..15) of tile t in lane l is centre 32t + 8(v/4) + 4h + (v%4) against row n.
 //
 // Accumulation (ACCUM), also on the matrix cores: per 64-row block, sums (centres x dims) += onehot^T (centres x
-// rows) x rows. The one-hot operand is exact in bf16 (0 or 1); each row value is split exactly into three bf16
+// rows) x rows. The one-hot operand is exact in bf16 (0 or 1, or 0 or 2 where it is read as bytes from LDS, the
+// sums then halved exactly at the fold); each row value is split exactly into three bf16
 // pieces (split3), so the float32 MFMA accumulators add the float32 row values themselves, rounded only by the
 // accumulation. Counts are LDS integer adds (exact, order-free). The block's inertia partial is a per-lane Kahan sum
 // of the rows' distances. With BEST every row's distance is the exact direct form (labels, best outputs); without
@@ -29,6 +30,7 @@
 #include <math.h>
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ the fused kernel
@@ -72,6 +74,12 @@ __device__ __forceinline__ void own_halves_u(uint32_t va, uint32_t vb, uint32_t 
     h0 = r[0];
     h1 = r[1];
 }
+// orders this wave's LDS accesses (every lane's earlier reads and writes before any later one)
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 // value of lane l ^ 32
 __device__ __forceinline__ float partner(float v, int lane) {
     const auto r = __builtin_amdgcn_permlane32_swap(u32(v), u32(v), false, false);
@@ -94,17 +102,30 @@ struct Geo {
     static constexpr int AS = D + 1;                // LDS row stride of the accumulators
 };
 
-// Screen one 32-row tile: x is this lane's half row. Returns the smallest and second smallest packed key over
-// this lane's 16 KT screen values.
+// This lane's half row as the screen's B operand (bf16, rounded to nearest), and |bf16(x)|^2 of the half row
+// from v_dot2_f32_bf16 on the same pairs.
 template <int D, int KP>
-__device__ __forceinline__ void screen_tile(const float (&x)[Geo<D, KP>::DH], const bf16x8 (&Aop)[Geo<D, KP>::KT][Geo<D, KP>::AK],
+__device__ __forceinline__ float make_b(const float (&x)[Geo<D, KP>::DH], bf16x8 (&B)[Geo<D, KP>::DS]) {
+    using G = Geo<D, KP>;
+    float s = 0.0f;
+#pragma unroll
+    for (int st = 0; st < G::DS; st++) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) B[st][q] = (__bf16)x[8 * st + q];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const bf16x2 v = {B[st][2 * p], B[st][2 * p + 1]};
+            s = __builtin_amdgcn_fdot2_f32_bf16(v, v, s, false);
+        }
+    }
+    return s;
+}
+
+// Screen one 32-row tile: B is this lane's half row. Returns the KT accumulators (16 screen values each).
+template <int D, int KP>
+__device__ __forceinline__ void screen_tile(const bf16x8 (&B)[Geo<D, KP>::DS], const bf16x8 (&Aop)[Geo<D, KP>::KT][Geo<D, KP>::AK],
                                             const bf16x8 &Bone, f32x16 (&a)[Geo<D, KP>::KT]) {
     using G = Geo<D, KP>;
-    bf16x8 B[G::DS];
-#pragma unroll
-    for (int s = 0; s < G::DS; s++)
-#pragma unroll
-        for (int q = 0; q < 8; q++) B[s][q] = (__bf16)x[8 * s + q];
     const f32x16 zero = {};
 #pragma unroll
     for (int t = 0; t < G::KT; t++) {
@@ -134,21 +155,24 @@ __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], flo
         }
 }
 
-// candidate bits of this lane's screen values against threshold T: bit (8(v/4) + 4h + v%4) of word t
+// Candidate bits of this lane's screen values: bit (8(v/4) + 4h + v%4) of word t is set when a[t][v] <= T2. The
+// values are compared unpacked; T2 = T + 4 RHO |T| + tiny covers the packing perturbation, so the set contains
+// every centre the packed-key test would admit. Two instructions per value: v_cmp into vcc, then v_addc shifts
+// the bit in (m = 2m + vcc), v = 15 first so bit v lands at position v; a nibble-to-byte spread places them.
 template <int D, int KP>
-__device__ __forceinline__ void cand_bits(const f32x16 (&a)[Geo<D, KP>::KT], float T, float rho, int h,
+__device__ __forceinline__ void cand_bits(const f32x16 (&a)[Geo<D, KP>::KT], float T2, int h,
                                           uint32_t (&w)[Geo<D, KP>::KT]) {
     using G = Geo<D, KP>;
-    constexpr uint32_t IMASK = (1u << G::IB) - 1u;
 #pragma unroll
     for (int t = 0; t < G::KT; t++) {
         uint32_t m = 0;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const float key = f32((u32(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
-            if (key - rho * fabsf(key) <= T) m |= 1u << (8 * (v >> 2) + 4 * h + (v & 3));
-        }
-        w[t] = m;
+        for (int v = 15; v >= 0; v--)
+            asm("v_cmp_ge_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc" : "+v"(m) : "v"(T2), "v"(a[t][v]) : "vcc");
+        // byte j = nibble j of the 16-bit mask
+        const uint32_t p = __builtin_amdgcn_perm(m, m, 0x01010000u);   // bytes b0, b0, b1, b1
+        const uint32_t q = ((p & 0x000f000fu) | ((p >> 4) & 0x0f000f00u));
+        w[t] = q << (4 * h);
     }
 }
 
@@ -167,18 +191,34 @@ __device__ __forceinline__ void load_half(const float *__restrict__ X, int64_t r
     }
 }
 
-// Split x into three bf16 pieces with x = hi + mid + lo exactly (truncation: hi keeps the top 8 significant
-// bits, mid the next 8 of the remainder, lo the rest, which has at most 8 significant bits), and pack pairs.
+__device__ __forceinline__ bf16x2 as_bf2(uint32_t v) { return *reinterpret_cast<bf16x2 *>(&v); }
+__device__ __forceinline__ uint32_t bf2_u32(bf16x2 v) { return *reinterpret_cast<uint32_t *>(&v); }
+
+// Split x into three bf16 pieces with x = hi + mid + lo exactly, and pack pairs. hi is x truncated to its top 8
+// significant bits (never rounds up, so never overflows); r = x - hi is exact in float32 and has at most 16
+// significant bits; mid = bf16(r) rounded to nearest; lo = r - mid has at most 8 significant bits, so bf16(lo) is
+// exact. The residuals come from v_dot2_f32_bf16 with the pair (-1, 0) or (0, -1): x + (-1) hi + 0, whose products
+// are exact and whose sum is representable, so the instruction returns it exactly.
+// The two pairs are moved into scalar registers as 32-bit literals: an inline constant in a bf16-pair operand is
+// not reliably the pair one means.
 __device__ __forceinline__ void split3(const float (&x)[8], bf16x8 &ph, bf16x8 &pm, bf16x8 &pl) {
+    uint32_t cl, ch;
+    asm("s_mov_b32 %0, 0x0000bf80" : "=s"(cl));
+    asm("s_mov_b32 %0, 0xbf800000" : "=s"(ch));
+    const bf16x2 nlo = as_bf2(cl), nhi = as_bf2(ch);
     uint32_t h[4], m[4], l[4];
 #pragma unroll
     for (int p = 0; p < 4; p++) {
         const float a = x[2 * p], b = x[2 * p + 1];
-        const float ra = a - f32(u32(a) & 0xffff0000u), rb = b - f32(u32(b) & 0xffff0000u);
-        const float sa = ra - f32(u32(ra) & 0xffff0000u), sb = rb - f32(u32(rb) & 0xffff0000u);
         h[p] = __builtin_amdgcn_perm(u32(b), u32(a), 0x07060302u);
-        m[p] = __builtin_amdgcn_perm(u32(rb), u32(ra), 0x07060302u);
-        l[p] = __builtin_amdgcn_perm(u32(sb), u32(sa), 0x07060302u);
+        const float ra = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(h[p]), nlo, a, false);
+        const float rb = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(h[p]), nhi, b, false);
+        const bf16x2 mp = {(__bf16)ra, (__bf16)rb};
+        m[p] = bf2_u32(mp);
+        const float sa = __builtin_amdgcn_fdot2_f32_bf16(mp, nlo, ra, false);
+        const float sb = __builtin_amdgcn_fdot2_f32_bf16(mp, nhi, rb, false);
+        const bf16x2 lp = {(__bf16)sa, (__bf16)sb};
+        l[p] = bf2_u32(lp);
     }
     ph = *reinterpret_cast<bf16x8 *>(h);
     pm = *reinterpret_cast<bf16x8 *>(m);
@@ -261,6 +301,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     constexpr int FOLD = (KP * 32 * NT + 2 * KP) * 4; // bytes of the end-of-block fold per wave
     // per wave: two block buffers, 64 uint16 labels and KP uint32 counts during the loop, the fold after it
     constexpr int LOOPB = 2 * L::BUF + 128 + 4 * KP;
+    // one-hot bytes in the block buffer once its rows are in registers: KP rows of OHS bytes (64 rows + 8 bytes
+    // of padding, so the 32 lanes of a half-wave reading 8 bytes each start on distinct even banks)
+    constexpr int OHS = 72, OHB_BYTES = KP * OHS;
+    constexpr bool OHB = NT == 1 && OHB_BYTES <= L::BUF;
     constexpr int WBYTES = (LOOPB > FOLD + 4 * KP) ? LOOPB : FOLD + 4 * KP;
     // window constants
     constexpr int NACC = 2 * G::DP + 2;
@@ -270,7 +314,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     constexpr float RHO = (float)(1.01 * (double)(1 << G::IB) * 0x1p-23);
     constexpr float FLUSH = (float)(0x1p-123 * 16.0);
     constexpr float TINY = (float)((G::DP + 2) * 0x1p-118);
-    constexpr float XSQ_UP = (float)(1.0 + 2.0 * (D + 2) * 0x1p-24);
+    // |x|^2 <= |bf16(x)|^2 / (1 - 2^-8)^2 (each bf16(x_j) is within 2^-8 |x_j|), with slack for the float32
+    // accumulation of the v_dot2 sums; XSQ_FLOOR covers products below the smallest normal if they are flushed
+    constexpr float XSQ_UP = 1.0079f;
+    constexpr float XSQ_FLOOR = (float)(G::DP * 0x1p-126);
     constexpr uint32_t IMASK = (1u << G::IB) - 1u;
     static_assert(D == G::DP && D <= 64 && KP <= 128, "fused kernel serves dims 16, 32, 64 and k <= 128");
 
@@ -370,21 +417,19 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         read_half<D>(buf, 0, lane, xa);
         read_half<D>(buf, 1, lane, xb);
         // ---- screens of tiles A and B
-        float sa = 0.0f, sb = 0.0f;
-#pragma unroll
-        for (int q = 0; q < DH; q++) {
-            sa = __builtin_fmaf(xa[q], xa[q], sa);
-            sb = __builtin_fmaf(xb[q], xb[q], sb);
-        }
-        float m1a, m2a, m1b, m2b;
+        float m1a, m2a, m1b, m2b, sa, sb;
         {
+            bf16x8 B[DS];
+            sa = make_b<D, KP>(xa, B);
             f32x16 a[KT];
-            screen_tile<D, KP>(xa, Aop, Bone, a);
+            screen_tile<D, KP>(B, Aop, Bone, a);
             min2_keys<D, KP>(a, m1a, m2a);
         }
         {
+            bf16x8 B[DS];
+            sb = make_b<D, KP>(xb, B);
             f32x16 a[KT];
-            screen_tile<D, KP>(xb, Aop, Bone, a);
+            screen_tile<D, KP>(B, Aop, Bone, a);
             min2_keys<D, KP>(a, m1b, m2b);
         }
         // ---- the owned row's two halves
@@ -398,7 +443,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         const uint32_t kmb = u32(km) & IMASK;
         const int kt = (int)kmb >> 4, kv = (int)kmb & 15;
         const int cm = 32 * kt + 8 * (kv >> 2) + 4 * kh + (kv & 3);
-        const float xsq_up = (s0 + s1) * XSQ_UP;
+        const float xsq_up = __builtin_fmaf(s0 + s1, XSQ_UP, XSQ_FLOOR);
         const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
         const float E = BETA * nx * cnmax + GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
         const float akm = km + RHO * fabsf(km);
@@ -415,18 +460,23 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
             float ya[DH], yb[DH];
             read_half<D>(buf, 0, lane, ya);
             read_half<D>(buf, 1, lane, yb);
-            const float Tp = partner(T, lane);
-            const float TA = (lane < 32) ? T : Tp, TB = (lane < 32) ? Tp : T;
+            const float T2 = T + (4.0f * RHO * fabsf(T) + TINY);
+            const float Tp = partner(T2, lane);
+            const float TA = (lane < 32) ? T2 : Tp, TB = (lane < 32) ? Tp : T2;
             uint32_t wa[KT], wb[KT];
             {
+                bf16x8 B[DS];
+                (void)make_b<D, KP>(ya, B);
                 f32x16 a[KT];
-                screen_tile<D, KP>(ya, Aop, Bone, a);
-                cand_bits<D, KP>(a, TA, RHO, h, wa);
+                screen_tile<D, KP>(B, Aop, Bone, a);
+                cand_bits<D, KP>(a, TA, h, wa);
             }
             {
+                bf16x8 B[DS];
+                (void)make_b<D, KP>(yb, B);
                 f32x16 a[KT];
-                screen_tile<D, KP>(yb, Aop, Bone, a);
-                cand_bits<D, KP>(a, TB, RHO, h, wb);
+                screen_tile<D, KP>(B, Aop, Bone, a);
+                cand_bits<D, KP>(a, TB, h, wb);
             }
 #pragma unroll
             for (int t = 0; t < KT; t++) {
@@ -532,10 +582,47 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                 ine_s = tt;
             }
             if (valid) atomicAdd(&CNT[bl], 1u);   // integer adds: the order does not matter
+            if constexpr (OHB) {
+                // The block's rows in the accumulation's layout (lane = one dim, eight rows per K-step) go to
+                // registers first; then the block buffer holds the one-hot bytes: byte [c][r] = 0x40, the high
+                // byte of bf16 2.0, where row r has label c (one byte write per row instead of a compare per
+                // (row, centre)); the sums come out doubled, exactly, and the fold halves them.
+                float xv[4][8];
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) xv[ks][i] = (ln < D) ? read_elem<D>(buf, 16 * ks + 8 * h + i, ln) : 0.0f;
+                wave_sync();
+                char *ohb = wbase + cur;
+#pragma unroll
+                for (int i = lane; i < OHB_BYTES / 16; i += 64) reinterpret_cast<uint4 *>(ohb)[i] = uint4{0u, 0u, 0u, 0u};
+                wave_sync();
+                if (valid) ohb[bl * OHS + lane] = (char)0x40;
+                wave_sync();
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    bf16x8 OH[KT];
+#pragma unroll
+                    for (int t = 0; t < KT; t++) {
+                        const uint2 w = *reinterpret_cast<const uint2 *>(ohb + (32 * t + ln) * OHS + 16 * ks + 8 * h);
+                        const uint32_t o[4] = {__builtin_amdgcn_perm(w.y, w.x, 0x010c000cu),
+                                               __builtin_amdgcn_perm(w.y, w.x, 0x030c020cu),
+                                               __builtin_amdgcn_perm(w.y, w.x, 0x050c040cu),
+                                               __builtin_amdgcn_perm(w.y, w.x, 0x070c060cu)};
+                        OH[t] = *reinterpret_cast<const bf16x8 *>(o);
+                    }
+                    bf16x8 ph, pm, pl;
+                    split3(xv[ks], ph, pm, pl);
+#pragma unroll
+                    for (int t = 0; t < KT; t++) {
+                        sacc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], ph, sacc[t][0], 0, 0, 0);
+                        sacc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], pm, sacc[t][0], 0, 0, 0);
+                        sacc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], pl, sacc[t][0], 0, 0, 0);
+                    }
+                }
+            } else {
             L16[lane] = valid ? (uint16_t)bl : (uint16_t)0x4000u;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            wave_sync();
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 const int rbase = 16 * ks + 8 * h;           // this lane's 8 rows of the K-step
@@ -571,6 +658,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                         sacc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(OH[t], pl, sacc[t][u], 0, 0, 0);
                     }
                 }
+            }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -611,7 +699,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const int c = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-                F[c * (32 * NT) + 32 * u + ln] = sacc[t][u][v];
+                F[c * (32 * NT) + 32 * u + ln] = OHB ? 0.5f * sacc[t][u][v] : sacc[t][u][v];
             }
     __syncthreads();
     const int64_t kw = (int64_t)k * W;
