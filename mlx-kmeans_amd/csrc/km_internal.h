@@ -87,6 +87,7 @@ hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X,
 // Fused single-read pass for dims <= 16: exact rows loop + deterministic accumulation into per-block partials.
 struct km_lowd_plan {
     int ok;          // 0 if the shape is not served (dims > 16, LDS too small, misaligned rows)
+    int screen;      // 1: float32 expanded-form screen + window, direct form on the winner only
     int64_t rbs;     // rows per block
     int nrb;         // blocks
     size_t lds;      // dynamic LDS bytes

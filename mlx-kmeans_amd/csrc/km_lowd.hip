@@ -2,10 +2,20 @@
 // read of X, the job of the reference's fused and one-hot kernels (core.py:1478-1534, 1562-1675) for the
 // low-d / large-n regime.
 //
-// Assignment. Each lane owns whole rows and runs the rows loop itself (core.py:263-274): for every centre in
-// ascending order, s = sum_j (x_j - c_j)^2 with j ascending, product and add rounded separately, kept when
-// s < best. Labels and best are therefore the rows loop's, bit for bit. Centres sit in LDS and are read by
-// broadcast; each centre read serves the R rows a lane holds.
+// Assignment. Each lane owns whole rows. Without the screen it runs the rows loop itself (core.py:263-274): for
+// every centre in ascending order, s = sum_j (x_j - c_j)^2 with j ascending, product and add rounded separately,
+// kept when s < best. With the screen (k >= 24) it first computes the expanded form a_c = |c|^2 - 2 x.c for every
+// centre as a float32 FMA chain (d FMAs instead of the direct form's 3d operations), keeps the smallest and second
+// smallest key (the centre index packed into the low mantissa bits), and proves with a rigorous error window that
+// no other centre can hold the row's minimum; the direct form then runs on that one centre only. Rows the window
+// cannot settle, and non-finite rows, run the full rows loop. Labels and best are the rows loop's, bit for bit,
+// either way. Centres sit in LDS and are read by broadcast; each centre read serves the R rows a lane holds.
+//
+// Window. |fl(a_c) - A_c| <= E = gamma_{D+2} (max|c|^2 + 2 max|c| |x|) for every c (D FMA roundings over terms
+// bounded by |c|^2 + 2 |x||c|, and |c|^2 itself rounded once from float64). The direct form s_c satisfies
+// |s_c - D_c| <= g D_c (g = gamma_{D+2}), so a centre other than the screen's minimiser m can hold the minimum
+// only if a_c - a_m <= 2E + 2 g/(1-g) D_m, with D_m <= |x|^2 + a_m + E; the packed index perturbs a key by at
+// most RHO relative, which the test absorbs.
 //
 // Accumulation, deterministic by construction. A block is one wave. Every lane has a private float32 tile
 // [count, best, x_0 .. x_{D-1}] x k clusters in LDS, laid out [cluster][column][lane]: a lane adds its row
@@ -29,10 +39,21 @@ struct LowGeo {
 
 __host__ __device__ constexpr size_t km_al16(size_t v) { return (v + 15) / 16 * 16; }
 
-// LDS bytes of one block (one wave): centres, the 64 lane tiles, the float64 accumulators
-__host__ __device__ inline size_t km_lowd_lds(int d, int k) {
+// LDS bytes of one block (one wave): centres, the 64 lane tiles, the float64 accumulators, and with the screen
+// the centres as [-2c, |c|^2] rows
+__host__ __device__ inline size_t km_lowd_lds(int d, int k, bool screen) {
     const size_t kw = (size_t)k * (d + 2);
-    return km_al16((size_t)k * d * 4) + kw * 64 * 4 + kw * 8;
+    return km_al16((size_t)k * d * 4) + kw * 64 * 4 + kw * 8 + (screen ? km_al16((size_t)k * (d + 1) * 4) : 0);
+}
+
+__host__ __device__ constexpr double km_lowd_gamma(int m) {
+    return m * 5.9604644775390625e-08 / (1.0 - m * 5.9604644775390625e-08);
+}
+
+__device__ __forceinline__ float lowd_vmin(float a, float b) {
+    float r;
+    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 
 // Largest k * (d + 2) served: the tiles take 256 bytes per entry.
@@ -86,7 +107,7 @@ __device__ __forceinline__ void fold_tiles(float *T, double *F, int kw, int lane
     wave_sync_lds();
 }
 
-template <int D>
+template <int D, bool SCR>
 __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, int64_t n,
                                                    const float *__restrict__ C, int k, int64_t rbs,
                                                    uint32_t *__restrict__ labels, float *__restrict__ best,
@@ -94,6 +115,17 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                                                    const int32_t *__restrict__ stop) {
     using G = LowGeo<D>;
     constexpr int W = G::W, R = G::R;
+    // Window constants, in coordinates shifted by o (the centres' mean): x' = fl(x - o), c' = fl(c - o). The screen
+    // a'_c = |c'|^2 - 2 x'.c' (FMA chain) is within E <= gE (|c'|^2 + 2 |x'||c'|) <= gE (2 max|c'|^2 + |x'|^2) of
+    // |c~|^2 - 2 x~.c~ for the exact shifts x~ = x - o, c~ = c - o (D roundings of the chain, one of |c'|^2, and
+    // the shifts' own roundings of at most u relative: gE = gamma_{D+5}), and D_c = |x~|^2 + |c~|^2 - 2 x~.c~. The
+    // direct form is within gd = gamma_{D+2}/(1-gamma_{D+2}) relative. Margin = 2E + 2 gd (|x~|^2 + |a'_m| + E),
+    // with |x~|^2 <= |x'|^2 (1 + 2 gamma_D + 4u), every coefficient inflated by 2^-18 for the float32 evaluation:
+    // W_X |x'|^2 + W_A |a'_m| + w_c.
+    constexpr double gE = km_lowd_gamma(D + 5), g2 = km_lowd_gamma(D + 2), gd = g2 / (1.0 - g2), up = 1.0 + 0x1p-18;
+    constexpr float W_X = (float)((2.0 * gE + 2.0 * gd * (1.0 + gE)) * (1.0 + 2.0 * km_lowd_gamma(D) + 0x1p-22) * up);
+    constexpr float W_A = (float)(2.0 * gd * up);
+    constexpr float TINY = (float)((D + 2) * 0x1p-118);
     if (stop && *stop) return;
     extern __shared__ float lds[];
     const int lane = threadIdx.x;
@@ -101,10 +133,46 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
     float *Cl = lds;
     float *T = lds + km_al16((size_t)k * D * 4) / 4;                      // [kw][64]
     double *F = reinterpret_cast<double *>(T + (size_t)kw * 64);          // [kw]
+    float *Q = reinterpret_cast<float *>(F + kw);                         // [k][D + 1]: -2c, |c|^2 (screen)
 
     for (int e = lane; e < k * D; e += 64) Cl[e] = C[e];
     for (int e = lane; e < kw * 64; e += 64) T[e] = 0.0f;
     for (int e = lane; e < kw; e += 64) F[e] = 0.0;
+    // screen constants: the shift o, max |c'| (rounded up), max |c'|^2, and the index bits packed into keys
+    float cnmax = 0.0f, csqmax = 0.0f;
+    float o[D];
+    int ib = 1;
+    if constexpr (SCR) {
+        wave_sync_lds();
+#pragma unroll
+        for (int j = 0; j < D; j++) {
+            double t = 0.0;
+            for (int c = 0; c < k; c++) t += (double)Cl[c * D + j];
+            o[j] = (float)(t / k);
+        }
+        for (int c = lane; c < k; c += 64) {
+            double sq = 0.0;
+#pragma unroll
+            for (int j = 0; j < D; j++) {
+                const float v = C[c * D + j] - o[j];
+                sq += (double)v * (double)v;
+                Q[c * (D + 1) + j] = -2.0f * v;
+            }
+            const float sf = (float)sq;
+            Q[c * (D + 1) + D] = sf;
+            cnmax = fmaxf(cnmax, (float)(sqrt(sq) * (1.0 + 1e-6)));
+            csqmax = fmaxf(csqmax, sf);
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            cnmax = fmaxf(cnmax, __shfl_xor(cnmax, off));
+            csqmax = fmaxf(csqmax, __shfl_xor(csqmax, off));
+        }
+        while ((1 << ib) < k) ib++;
+    }
+    const uint32_t imask = (1u << ib) - 1u;
+    const float rho = (float)(1.01 * (double)(1 << ib) * 0x1p-23);
+    const float csq2 = fmaxf(csqmax, cnmax * cnmax) * 2.0f * (1.0f + 0x1p-20f);
+    const float w_c = (float)((2.0 * gE + 2.0 * gd * gE) * (1.0 + 0x1p-18)) * csq2 + 4.0f * TINY;
 
     const int64_t r_begin = (int64_t)blockIdx.x * rbs;
     const int64_t r_end = (r_begin + rbs < n) ? r_begin + rbs : n;
@@ -131,29 +199,126 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                 load_row<D>(X, row < r_end ? row : r_end - 1, xn[i]);
             }
         }
-        // the rows loop for R rows at once
         float bst[R];
         uint32_t bl[R];
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            bst[i] = INFINITY;
-            bl[i] = 0;
-        }
-        for (int c = 0; c < k; c++) {
-            float cc[D];
-#pragma unroll
-            for (int j = 0; j < D; j++) cc[j] = Cl[c * D + j];
+        if constexpr (SCR) {
+            // the screen: smallest and second smallest packed key of |c'|^2 - 2 x'.c' per row
+            float m1[R], m2[R], xs[R][D];
 #pragma unroll
             for (int i = 0; i < R; i++) {
+                m1[i] = 3.4e38f;
+                m2[i] = 3.4e38f;
+#pragma unroll
+                for (int j = 0; j < D; j++) xs[i][j] = xr[i][j] - o[j];
+            }
+            for (int c = 0; c < k; c++) {
+                float q[D + 1];
+#pragma unroll
+                for (int j = 0; j <= D; j++) q[j] = Q[c * (D + 1) + j];
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    float a = q[D];
+#pragma unroll
+                    for (int j = 0; j < D; j++) a = __builtin_fmaf(xs[i][j], q[j], a);
+                    const float key = __uint_as_float((__float_as_uint(a) & ~imask) | (uint32_t)c);
+                    m2[i] = __builtin_amdgcn_fmed3f(m1[i], m2[i], key);
+                    m1[i] = lowd_vmin(m1[i], key);
+                }
+            }
+            bool full[R];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                float xsq = 0.0f;
+#pragma unroll
+                for (int j = 0; j < D; j++) xsq = __builtin_fmaf(xs[i][j], xs[i][j], xsq);
+                const float km = m1[i];
+                const float akm = __builtin_fmaf(rho, fabsf(km), km);
+                // margin 2E + 2 GDIR D_m with E <= GAM (max|c|^2 + max|c|^2 + |x|^2) (2ab <= a^2 + b^2) and
+                // D_m <= |x|^2 + |a_m| + E: linear in |x|^2 and |a_m|, constants folded on the host side of it
+                const float margin = __builtin_fmaf(W_X, xsq, __builtin_fmaf(W_A, fabsf(akm), w_c));
+                float Tw = akm + margin;
+                Tw = __builtin_fmaf(0x1p-22f, fabsf(Tw), Tw);
+                const uint32_t cm = __float_as_uint(km) & imask;
+                const uint32_t cmc = cm < (uint32_t)k ? cm : 0u;
                 float s = 0.0f;
 #pragma unroll
                 for (int j = 0; j < D; j++) {
-                    const float t = xr[i][j] - cc[j];
+                    const float t = xr[i][j] - Cl[cmc * D + j];
                     s = s + t * t;
                 }
-                if (s < bst[i]) {
-                    bst[i] = s;
-                    bl[i] = (uint32_t)c;
+                // settled: no second centre inside the window, a finite row (xsq) and distance, an index below k
+                const bool settled = __builtin_fmaf(-rho, fabsf(m2[i]), m2[i]) > Tw && xsq < INFINITY &&
+                                     s < INFINITY && cm < (uint32_t)k;
+                full[i] = !settled;
+                bst[i] = s;
+                bl[i] = cmc;
+            }
+            // Rows the window leaves open run the rows loop with the whole wave: the row is broadcast, every lane
+            // scores its centres (lane, lane + 64, ...) in the direct form, and the wave keeps the smallest
+            // distance, the lowest index among equal ones - the rows loop's result, including label 0 and best
+            // +inf when no distance is below +inf.
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                uint64_t need = __ballot(full[i]);
+                while (need) {
+                    const int L = __builtin_ctzll(need);
+                    need &= need - 1;
+                    float xb[D];
+#pragma unroll
+                    for (int j = 0; j < D; j++)
+                        xb[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xr[i][j]), L));
+                    float bv = INFINITY;
+                    uint32_t bi = 0;
+                    for (int c = lane; c < k; c += 64) {
+                        float sc = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < D; j++) {
+                            const float t = xb[j] - Cl[c * D + j];
+                            sc = sc + t * t;
+                        }
+                        if (sc < bv) {
+                            bv = sc;
+                            bi = (uint32_t)c;
+                        }
+                    }
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) {
+                        const float ov = __shfl_xor(bv, off);
+                        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, off);
+                        if (ov < bv || (ov == bv && oi < bi)) {
+                            bv = ov;
+                            bi = oi;
+                        }
+                    }
+                    if (lane == L) {
+                        bst[i] = bv;
+                        bl[i] = bi;
+                    }
+                }
+            }
+        } else {
+            // the rows loop for R rows at once
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                bst[i] = INFINITY;
+                bl[i] = 0;
+            }
+            for (int c = 0; c < k; c++) {
+                float cc[D];
+#pragma unroll
+                for (int j = 0; j < D; j++) cc[j] = Cl[c * D + j];
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < D; j++) {
+                        const float t = xr[i][j] - cc[j];
+                        s = s + t * t;
+                    }
+                    if (s < bst[i]) {
+                        bst[i] = s;
+                        bl[i] = (uint32_t)c;
+                    }
                 }
             }
         }
@@ -199,22 +364,30 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
 typedef void (*lowd_fn)(const float *, int64_t, const float *, int, int64_t, uint32_t *, float *, float *, float *,
                         int, const int32_t *);
 
-static lowd_fn g_lowd[17] = {nullptr,          k_fused_lowd<1>,  k_fused_lowd<2>,  k_fused_lowd<3>,
-                             k_fused_lowd<4>,  k_fused_lowd<5>,  k_fused_lowd<6>,  k_fused_lowd<7>,
-                             k_fused_lowd<8>,  k_fused_lowd<9>,  k_fused_lowd<10>, k_fused_lowd<11>,
-                             k_fused_lowd<12>, k_fused_lowd<13>, k_fused_lowd<14>, k_fused_lowd<15>,
-                             k_fused_lowd<16>};
+#define KM_LOWD_FNS(S)                                                                                        \
+    {nullptr,              k_fused_lowd<1, S>,  k_fused_lowd<2, S>,  k_fused_lowd<3, S>,  k_fused_lowd<4, S>,  \
+     k_fused_lowd<5, S>,  k_fused_lowd<6, S>,  k_fused_lowd<7, S>,  k_fused_lowd<8, S>,  k_fused_lowd<9, S>,   \
+     k_fused_lowd<10, S>, k_fused_lowd<11, S>, k_fused_lowd<12, S>, k_fused_lowd<13, S>, k_fused_lowd<14, S>,  \
+     k_fused_lowd<15, S>, k_fused_lowd<16, S>}
+static lowd_fn g_lowd[2][17] = {KM_LOWD_FNS(false), KM_LOWD_FNS(true)};
+#undef KM_LOWD_FNS
 
 static int g_lowd_cus = 0;
 
 static int lowd_rows_per_iter(int d) { return 64 * (d <= 4 ? 8 : d <= 8 ? 4 : 2); }
+
+// The screen costs d + 3 operations per centre and row against the direct form's 3d + 3, plus a per-row window
+// and one direct form with an LDS gather; measured on MI355X it is the faster of the two from about 24 centres on
+// (20M rows: d = 4, k = 32 -21 %; d = 2, k = 48 -15 %) and not below (d = 4, k = 12 +5 %; d = 8, k = 8 +1 %).
+static bool lowd_screen(int k) { return k >= 24; }
 
 km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
     km_lowd_plan pl{};
     if (d < 1 || d > 16 || k < 1 || n < 1) return pl;
     if ((int64_t)k * (d + 2) > KM_LOWD_MAX_KW) return pl;
     if ((d % 2 == 0) && !aligned) return pl;   // vector row loads need 8/16-byte aligned rows
-    const size_t lds = km_lowd_lds(d, k);
+    const bool scr = lowd_screen(k);
+    const size_t lds = km_lowd_lds(d, k, scr);
     if (g_lowd_cus == 0) {
         int dev = 0;
         hipDeviceProp_t prop;
@@ -224,7 +397,7 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
     }
     if (lds > 65536) return pl;
     int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)g_lowd[d], 64, lds) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)g_lowd[scr][d], 64, lds) != hipSuccess ||
         occ < 1)
         occ = 1;
     const int64_t unit = lowd_rows_per_iter(d);
@@ -235,6 +408,7 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
     int64_t rbs = (n + nrb - 1) / nrb;
     rbs = (rbs + unit - 1) / unit * unit;
     pl.ok = 1;
+    pl.screen = scr ? 1 : 0;
     pl.rbs = rbs;
     pl.nrb = (int)((n + rbs - 1) / rbs);
     pl.lds = lds;
@@ -245,7 +419,7 @@ hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s) {
     if (!pl.ok || d < 1 || d > 16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(g_lowd[d], dim3(pl.nrb), dim3(64), pl.lds, s, X, n, C, k, pl.rbs, labels, best, psum,
-                       pcomp, rb0, stop);
+    hipLaunchKernelGGL(g_lowd[pl.screen ? 1 : 0][d], dim3(pl.nrb), dim3(64), pl.lds, s, X, n, C, k, pl.rbs, labels,
+                       best, psum, pcomp, rb0, stop);
     return hipGetLastError();
 }

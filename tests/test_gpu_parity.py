@@ -134,7 +134,7 @@ def test_fit_loop_matches_oracle(lib, name):
 
 @pytest.mark.parametrize("d,k", [(32, 64), (16, 64), (32, 32), (64, 32), (16, 32), (32, 40), (16, 8), (12, 20),
                                  (8, 8), (5, 33), (4, 12), (3, 7), (2, 64), (1, 5), (48, 100), (96, 33), (200, 64),
-                                 (17, 5), (768, 40), (33, 300)])
+                                 (17, 5), (768, 40), (33, 300), (4, 32), (2, 48), (1, 70), (3, 40), (6, 27)])
 def test_paths_are_bit_identical(lib, d, k):
     """Every path that serves a shape returns the rows path's labels and best bit for bit and the same counts;
     sums agree to the accumulation tolerance. 60,011 rows: a ragged tail for every block size."""
@@ -158,6 +158,45 @@ def test_paths_are_bit_identical(lib, d, k):
         cnt = np.maximum(np.rint(t1[:, 0]), 1)[:, None]
         assert np.max(np.abs(t1[:, 2:] - t2[:, 2:]) / cnt) / scale <= CENTRE_TOL, name
         np.testing.assert_allclose(t2[:, 1], t1[:, 1], rtol=1e-6, atol=1e-30)
+    ctx.close()
+
+
+@pytest.mark.parametrize("d,k", [(4, 32), (1, 70), (32, 64), (16, 32), (48, 100)])
+def test_screen_edge_cases_match_the_rows_loop(lib, d, k):
+    """The screened paths against the rows loop and the oracle on the cases a screen can get wrong: duplicate
+    centres (exact ties, lowest index wins), rows equal to a centre (distance 0), NaN and infinite rows (label 0,
+    best +inf or NaN as the rows loop leaves them), rows whose float32 distances overflow, and a zero row."""
+    import oracle
+    rng = np.random.default_rng(17 + d + k)
+    n = 20_000
+    cen = rng.uniform(-4, 4, size=(max(k // 3, 2), d)).astype(np.float32)
+    X = (cen[rng.integers(0, len(cen), n)] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(n, k, replace=False)].copy()
+    C[5] = C[3]                                   # duplicate centres: ties go to index 3
+    X[10:20] = C[3]                               # distance 0 to both duplicates
+    X[20:30] = C[7]
+    X[30] = np.nan
+    X[31, 0] = np.inf
+    X[32, -1] = -np.inf
+    X[33] = 3.0e19                                # (x - c)^2 overflows for every centre
+    X[34, 0] = 2.0e19
+    X[35] = 0.0
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] screen edge cases d={d} k={k}")
+    t1, l1, b1 = ctx.run_pass(C, path=lib.KM_PATH_ROWS, labels=True, best=True)
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(l1, ol) and np.array_equal(b1.view(np.uint32), ob.view(np.uint32))
+    served = 0
+    for name in ("mfma", "fused"):
+        if not SERVED[name](d, k):
+            continue
+        served += 1
+        t2, l2, b2 = ctx.run_pass(C, path=lib.PATHS[name], labels=True, best=True)
+        assert ctx.last_path() == name
+        assert np.array_equal(l1, l2), (name, np.flatnonzero(l1 != l2)[:10])
+        assert np.array_equal(b1.view(np.uint32), b2.view(np.uint32)), name
+    assert served
     ctx.close()
 
 
