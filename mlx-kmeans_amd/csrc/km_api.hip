@@ -402,6 +402,8 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, c->red.ensure((size_t)S * kw));
     uint32_t *lab_all = labels_d ? labels_d : c->labels.p;
     float *best_all = best_d ? best_d : c->best.p;
+    // without per-row outputs, single-candidate rows skip the rescoring and the accumulation adds the distances
+    const int lite = (labels_d || best_d) ? 0 : 1;
     HIPCHK(c, launch(c, KK_BIG_PREP, [&] {
         return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop, c->stream);
     }));
@@ -420,11 +422,12 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
         }));
         HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {
             return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->ctl,
-                                         lab_all + row0, best_all + row0, stop, c->stream);
+                                         lab_all + row0, best_all + row0, lite, stop, c->stream);
         }));
         HIPCHK(c, launch(c, KK_BIG_ACCUM, [&] {
-            return km_launch_big_accum(bp, p.X, p.rows, d, lab_all + row0, best_all + row0, k, c->hist.p,
-                                       c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw, stop, c->stream);
+            return km_launch_big_accum(bp, p.X, p.rows, d, lab_all + row0, best_all + row0, lite ? Cin : nullptr, k,
+                                       c->hist.p, c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw, stop,
+                                       c->stream);
         }));
         row0 += p.rows;
     }

@@ -388,11 +388,13 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
 // so lanes on different rows or items read different banks), the next chunk's loads in flight in registers while
 // the current chunk is used; every item carries its running direct-form sum across the chunks, so the dims are
 // added in ascending order. Then one thread per row takes its items in order with a strict '<': the rows loop
-// restricted to the candidates. Rows marked KB_OVER are left to k_big_fullscan.
+// restricted to the candidates. Rows marked KB_OVER are left to k_big_fullscan. With LITE (passes that return no
+// per-row distances) rows with a single candidate take it as their label without a distance - the sorted
+// accumulation adds their distances - and only rows with several candidates are rescored.
 static constexpr int KB_RR = 64;      // rows per rescoring block
 static constexpr int KB_RT = 256;     // threads (= items per round) per rescoring block
 static constexpr int KB_RCH = 32;     // dims per LDS chunk
-template <bool V4>
+template <bool V4, bool LITE>
 __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__ X, int64_t n, int d,
                                                        const float *__restrict__ C, int k,
                                                        const uint16_t *__restrict__ ncand,
@@ -414,6 +416,11 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
     if (tid < KB_RR && tid < nr) {
         code = ncand[r0 + tid];
         cntr = code == KB_OVER ? 0 : (code & 255) + (code >> 8);
+        if (LITE && cntr == 1) {
+            labels[r0 + tid] = cand[(r0 + tid) * KB_CAP + ((code & 255) ? 0 : KB_HALF)];
+            cntr = 0;
+            code = KB_OVER;   // nothing more for this row here
+        }
     }
     if (tid < 64) {
         int incl = cntr;
@@ -715,10 +722,15 @@ __global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict_
     }
 }
 
-// Block per cluster (KB_SEGW waves, each a fixed consecutive range of the cluster's rows): entries [count, best, x_0 .. x_{d-1}] as float64 sums over the cluster's rows
-// in ascending row order, written to tmp[c * (d + 2) + e].
+// Block per cluster (KB_SEGW waves, each a fixed consecutive range of the cluster's rows): entries [count, best,
+// x_0 .. x_{d-1}] as float64 sums over the cluster's rows in ascending row order, written to tmp[c * (d + 2) + e].
+// With LITE the best column is not read from best[]: each lane adds (x_j - c_j)^2 over its dims for every row (FMA
+// form, float32 per row, float64 across rows) and the wave adds its lanes in a fixed butterfly - the cluster's
+// inertia, equal to the sum of the rows' direct-form distances to float32 rounding.
 static constexpr int KB_SEGW = 8;
+template <bool LITE>
 __global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__restrict__ X, int d, const float *__restrict__ best,
+                                                     const float *__restrict__ C,
                                                      const uint32_t *__restrict__ perm, int64_t r0,
                                                      const uint32_t *__restrict__ counts,
                                                      const uint32_t *__restrict__ base, int k,
@@ -737,6 +749,15 @@ __global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__rest
     double acc[MAXJ];
 #pragma unroll
     for (int i = 0; i < MAXJ; i++) acc[i] = 0.0;
+    float cv[LITE ? MAXJ : 1];
+    double accb = 0.0;
+    if constexpr (LITE) {
+#pragma unroll
+        for (int i = 0; i < MAXJ; i++) {
+            const int j = lane + 64 * i;
+            cv[i] = j < d ? C[(int64_t)c * d + j] : 0.0f;
+        }
+    }
     // rows in order; the row indices of the next 8 are loaded ahead, and each row's values are loaded before
     // they are added
     uint32_t pf[8];
@@ -757,12 +778,27 @@ __global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__rest
 #pragma unroll
                 for (int i = 0; i < MAXJ; i++) {
                     const int j = lane + 64 * i;
-                    v[i] = j < d ? x[j] : (j == d ? best[r] : 0.0f);
+                    v[i] = j < d ? x[j] : ((!LITE && j == d) ? best[r] : 0.0f);
                 }
 #pragma unroll
                 for (int i = 0; i < MAXJ; i++) acc[i] += (double)v[i];
+                if constexpr (LITE) {
+                    float ds = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < MAXJ; i++) {
+                        const float t = v[i] - cv[i];   // 0 - 0 past the last dim
+                        ds = __builtin_fmaf(t, t, ds);
+                    }
+                    accb += (double)ds;
+                }
             }
         }
+    }
+    if constexpr (LITE) {
+        for (int off = 32; off > 0; off >>= 1) accb += __shfl_xor(accb, off);
+#pragma unroll
+        for (int i = 0; i < MAXJ; i++)
+            if (lane + 64 * i == d) acc[i] = accb;
     }
 #pragma unroll
     for (int i = 0; i < MAXJ; i++) {
@@ -862,10 +898,12 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
 
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, km_control *ctl, uint32_t *labels,
-                                 float *best, const int32_t *stop, hipStream_t s) {
+                                 float *best, int lite, const int32_t *stop, hipStream_t s) {
     const bool v4 = (d % 4 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)C % 16 == 0);
-    hipLaunchKernelGGL(v4 ? k_big_rescore<true> : k_big_rescore<false>, dim3((unsigned)((n + KB_RR - 1) / KB_RR)),
-                       dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand, labels, best, stop);
+    auto fn = v4 ? (lite ? k_big_rescore<true, true> : k_big_rescore<true, false>)
+                 : (lite ? k_big_rescore<false, true> : k_big_rescore<false, false>);
+    hipLaunchKernelGGL(fn, dim3((unsigned)((n + KB_RR - 1) / KB_RR)), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
+                       labels, best, stop);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), (size_t)d * 4, s, X, d, C, k, over, ctl, labels, best,
@@ -874,8 +912,8 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
 }
 
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
-                               const float *best, int k, uint32_t *H, uint32_t *counts, uint32_t *base,
-                               uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
+                               const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
+                               uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
     hipLaunchKernelGGL(k_big_hist, dim3(pl.nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -884,7 +922,8 @@ hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n,
     hipLaunchKernelGGL(k_big_scatter, dim3(pl.nb), dim3(256), (size_t)(k + 256) * 4, s, labels, n, k, H, base, perm,
                        stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_segsum, dim3(k), dim3(64 * KB_SEGW), (size_t)KB_SEGW * (d + 1) * 8, s, X, d, best, perm,
-                       (int64_t)0, counts, base, k, tmp, stop);
+    hipLaunchKernelGGL(C_lite ? k_big_segsum<true> : k_big_segsum<false>, dim3(k), dim3(64 * KB_SEGW),
+                       (size_t)KB_SEGW * (d + 1) * 8, s, X, d, best, C_lite, perm, (int64_t)0, counts, base, k, tmp,
+                       stop);
     return hipGetLastError();
 }

@@ -118,9 +118,11 @@ hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, i
 hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
                                 int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
                                 uint32_t *over, km_control *ctl, const int32_t *stop, hipStream_t s);
+// lite: the pass returns no per-row distances; single-candidate rows take their label without one
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, km_control *ctl, uint32_t *labels,
-                                 float *best, const int32_t *stop, hipStream_t s);
+                                 float *best, int lite, const int32_t *stop, hipStream_t s);
+// C_lite non-null: the best column is the rows' FMA-form distances to C, not best[] (pair with a lite rescore)
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
-                               const float *best, int k, uint32_t *H, uint32_t *counts, uint32_t *base,
-                               uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s);
+                               const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
+                               uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s);
