@@ -77,7 +77,7 @@ struct km_ctx {
     DBuf<float> bcsq, bcn, bmax;
     DBuf<uint16_t> ncand;
     DBuf<uint16_t> cand;
-    DBuf<uint32_t> hist, counts, base, perm, over;
+    DBuf<uint32_t> hist, counts, base, perm, over, multi;
     DBuf<float> Cb[2];      // centre buffers (k, d): pass p reads Cb[p & 1], writes Cb[(p + 1) & 1]
     DBuf<float> psum, pcomp;
     DBuf<double> tot;
@@ -207,6 +207,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->base.release();
     c->perm.release();
     c->over.release();
+    c->multi.release();
     c->red.release();
     c->labels.release();
     c->best.release();
@@ -395,6 +396,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, c->base.ensure((size_t)k));
     HIPCHK(c, c->perm.ensure((size_t)max_rows));
     HIPCHK(c, c->over.ensure((size_t)max_rows));
+    HIPCHK(c, c->multi.ensure((size_t)max_rows));
     HIPCHK(c, c->labels.ensure((size_t)c->n));
     HIPCHK(c, c->best.ensure((size_t)c->n));
     HIPCHK(c, c->tot.ensure((size_t)kw));
@@ -418,11 +420,11 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
             }));
         HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
             return km_launch_big_screen(bp, mode, p.x16, p.xsq, p.rows, d, c->cop.p, c->bmax.p, k, c->ncand.p,
-                                        c->cand.p, c->over.p, c->ctl, stop, c->stream);
+                                        c->cand.p, c->over.p, c->multi.p, c->ctl, stop, c->stream);
         }));
         HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {
-            return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->ctl,
-                                         lab_all + row0, best_all + row0, lite, stop, c->stream);
+            return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->multi.p,
+                                         c->ctl, lab_all + row0, best_all + row0, lite, stop, c->stream);
         }));
         HIPCHK(c, launch(c, KK_BIG_ACCUM, [&] {
             return km_launch_big_accum(bp, p.X, p.rows, d, lab_all + row0, best_all + row0, lite ? Cin : nullptr, k,

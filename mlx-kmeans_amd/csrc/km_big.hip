@@ -118,7 +118,10 @@ __global__ __launch_bounds__(256) void k_big_cnorm(const float *__restrict__ C, 
                                                    float *__restrict__ csq, float *__restrict__ cn,
                                                    km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
-    if (blockIdx.x == 0 && threadIdx.x == 0) ctl->n_over = 0;   // rows the next screen lists for a full scan
+    if (blockIdx.x == 0 && threadIdx.x == 0) {   // rows the next screen lists for a full scan / a rescoring
+        ctl->n_over = 0;
+        ctl->n_multi = 0;
+    }
     const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (c >= kpad) return;
@@ -228,7 +231,7 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
     int approx, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
-    km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
+    uint32_t *__restrict__ multi, km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
     constexpr int DP = 16 * DS, AK = DS + 1, NACC = DP + 2;
     constexpr float GACC = (float)(2.04 * kb_gamma(NACC) * (1.0 + 0x1p-20));
     constexpr float GAM2 = (float)((1.01 * kb_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
@@ -378,6 +381,16 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     }
     ncand[row] = (uint16_t)code;
     if (code == KB_OVER) over[atomicAdd(&ctl->n_over, 1u)] = (uint32_t)row;
+    // rows with several candidates: one counter update per wave, each row at its place among the wave's
+    const bool is_multi = code != KB_OVER && (code & 255) + (code >> 8) >= 2;
+    const uint64_t mm = __ballot(is_multi);
+    if (mm) {
+        const int leader = __ffsll((unsigned long long)mm) - 1;
+        uint32_t base = 0;
+        if (lane == leader) base = atomicAdd(&ctl->n_multi, (uint32_t)__popcll(mm));
+        base = (uint32_t)__shfl((int)base, leader);
+        if (is_multi) multi[base + (uint32_t)__popcll(mm & ((1ull << lane) - 1ull))] = (uint32_t)row;
+    }
 }
 
 // ------------------------------------------------------------------ exact rescoring
@@ -389,8 +402,8 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
 // the current chunk is used; every item carries its running direct-form sum across the chunks, so the dims are
 // added in ascending order. Then one thread per row takes its items in order with a strict '<': the rows loop
 // restricted to the candidates. Rows marked KB_OVER are left to k_big_fullscan. With LITE (passes that return no
-// per-row distances) rows with a single candidate take it as their label without a distance - the sorted
-// accumulation adds their distances - and only rows with several candidates are rescored.
+// per-row distances) the blocks take 64 entries at a time of the screen's list of rows with several candidates;
+// single-candidate rows take their label in k_big_label1, and the sorted accumulation adds the distances.
 static constexpr int KB_RR = 64;      // rows per rescoring block
 static constexpr int KB_RT = 256;     // threads (= items per round) per rescoring block
 static constexpr int KB_RCH = 32;     // dims per LDS chunk
@@ -399,9 +412,12 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                                                        const float *__restrict__ C, int k,
                                                        const uint16_t *__restrict__ ncand,
                                                        const uint16_t *__restrict__ cand,
+                                                       const uint32_t *__restrict__ list,
+                                                       const km_control *__restrict__ ctl,
                                                        uint32_t *__restrict__ labels, float *__restrict__ best,
                                                        const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
+    __shared__ uint32_t rid[KB_RR];   // the block's rows: consecutive, or entries of the list
     __shared__ float xs[KB_RR * (KB_RCH + 1)];
     __shared__ float cs[KB_RT * (KB_RCH + 1)];
     __shared__ uint16_t it_c[KB_RR * KB_CAP];
@@ -409,18 +425,17 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
     __shared__ float it_s[KB_RR * KB_CAP];
     __shared__ int first[KB_RR + 1];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int64_t r0 = (int64_t)blockIdx.x * KB_RR;
-    const int nr = (int)((n - r0) < KB_RR ? (n - r0) : KB_RR);
+    const int64_t total = LITE ? (int64_t)ctl->n_multi : n;
+    for (int64_t r0 = (int64_t)blockIdx.x * KB_RR; r0 < total; r0 += (int64_t)gridDim.x * KB_RR) {
+    const int nr = (int)((total - r0) < KB_RR ? (total - r0) : KB_RR);
+    __syncthreads();   // the previous chunk's LDS is no longer read
+    if (tid < nr) rid[tid] = LITE ? list[r0 + tid] : (uint32_t)(r0 + tid);
+    __syncthreads();
     // item lists: thread r owns row r; an exclusive scan of the counts (wave 0) gives each row its slots
     int code = KB_OVER, cntr = 0;
     if (tid < KB_RR && tid < nr) {
-        code = ncand[r0 + tid];
+        code = ncand[rid[tid]];
         cntr = code == KB_OVER ? 0 : (code & 255) + (code >> 8);
-        if (LITE && cntr == 1) {
-            labels[r0 + tid] = cand[(r0 + tid) * KB_CAP + ((code & 255) ? 0 : KB_HALF)];
-            cntr = 0;
-            code = KB_OVER;   // nothing more for this row here
-        }
     }
     if (tid < 64) {
         int incl = cntr;
@@ -438,7 +453,7 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         for (int half = 0; half < 2; half++) {
             const int nc = half ? code >> 8 : code & 255;
             for (int i = 0; i < nc; i++) {
-                const uint16_t v = cand[(r0 + tid) * KB_CAP + half * KB_HALF + i];
+                const uint16_t v = cand[(int64_t)rid[tid] * KB_CAP + half * KB_HALF + i];
                 int j = m - 1;
                 while (j >= b && it_c[j] > v) { it_c[j + 1] = it_c[j]; j--; }
                 it_c[j + 1] = v;
@@ -474,7 +489,7 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                 for (int u = 0; u < XPT / 4; u++) {
                     const int r = tid / 8 + 32 * u, p = tid % 8;
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (r < nr && 4 * p < w) v = *reinterpret_cast<const float4 *>(X + (r0 + r) * d + j0 + 4 * p);
+                    if (r < nr && 4 * p < w) v = *reinterpret_cast<const float4 *>(X + (int64_t)rid[r] * d + j0 + 4 * p);
                     xv[4 * u] = v.x;
                     xv[4 * u + 1] = v.y;
                     xv[4 * u + 2] = v.z;
@@ -494,7 +509,7 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                 for (int u = 0; u < XPT; u++) {
                     const int e = tid + KB_RT * u;
                     const int r = e / KB_RCH, jj = e % KB_RCH;
-                    xv[u] = (r < nr && jj < w) ? X[(r0 + r) * d + j0 + jj] : 0.0f;
+                    xv[u] = (r < nr && jj < w) ? X[(int64_t)rid[r] * d + j0 + jj] : 0.0f;
                 }
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
@@ -550,9 +565,22 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
             const float sq = it_s[q];
             if (sq < bst) { bst = sq; bl = (uint32_t)it_c[q]; }
         }
-        labels[r0 + tid] = bl;
-        best[r0 + tid] = bst;
+        labels[rid[tid]] = bl;
+        best[rid[tid]] = bst;
     }
+    }
+}
+
+// Labels of the rows whose window held a single candidate (passes without per-row distances; the rescoring
+// takes the listed rows with several).
+__global__ __launch_bounds__(256) void k_big_label1(const uint16_t *__restrict__ ncand, const uint16_t *__restrict__ cand,
+                                                    int64_t n, uint32_t *__restrict__ labels,
+                                                    const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= n) return;
+    const int code = ncand[r];
+    if (code != KB_OVER && (code & 255) + (code >> 8) == 1) labels[r] = cand[r * KB_CAP + ((code & 255) ? 0 : KB_HALF)];
 }
 
 // Block per listed row: the rows loop over every centre. The row sits in LDS; 256 centres at a time are staged
@@ -819,7 +847,8 @@ __global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__rest
 // ------------------------------------------------------------------ planning and launch
 
 typedef void (*screen_fn)(const uint16_t *, const float *, int64_t, int, const uint16_t *, const float *, int, int,
-                          int, float, int, uint16_t *, uint16_t *, uint32_t *, km_control *, const int32_t *);
+                          int, float, int, uint16_t *, uint16_t *, uint32_t *, uint32_t *, km_control *,
+                          const int32_t *);
 
 static screen_fn kb_screen_for(int DS) {
     switch (DS) {
@@ -886,26 +915,37 @@ hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, i
 
 hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
                                 int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
-                                uint32_t *over, km_control *ctl, const int32_t *stop, hipStream_t s) {
+                                uint32_t *over, uint32_t *multi, km_control *ctl, const int32_t *stop, hipStream_t s) {
     screen_fn fn = kb_screen_for(pl.DS);
     if (!fn) return hipErrorInvalidValue;
     const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
     const unsigned blocks = (unsigned)((pl.ntiles + KB_WAVES - 1) / KB_WAVES);
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), 2 * KB_SLICE * 1024, s, X16T, xsq, n, d, Cop, maxes, k,
-                       pl.nchunks, pl.ib, rho, mode == KM_APPROX ? 1 : 0, ncand, cand, over, ctl, stop);
+                       pl.nchunks, pl.ib, rho, mode == KM_APPROX ? 1 : 0, ncand, cand, over, multi, ctl, stop);
     return hipGetLastError();
 }
 
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
-                                 const uint16_t *cand, const uint32_t *over, km_control *ctl, uint32_t *labels,
-                                 float *best, int lite, const int32_t *stop, hipStream_t s) {
+                                 const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
+                                 uint32_t *labels, float *best, int lite, const int32_t *stop, hipStream_t s) {
     const bool v4 = (d % 4 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)C % 16 == 0);
-    auto fn = v4 ? (lite ? k_big_rescore<true, true> : k_big_rescore<true, false>)
-                 : (lite ? k_big_rescore<false, true> : k_big_rescore<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)((n + KB_RR - 1) / KB_RR)), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
-                       labels, best, stop);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    const unsigned chunks = (unsigned)((n + KB_RR - 1) / KB_RR);
+    hipError_t e;
+    typedef void (*rescore_fn)(const float *, int64_t, int, const float *, int, const uint16_t *, const uint16_t *,
+                               const uint32_t *, const km_control *, uint32_t *, float *, const int32_t *);
+    if (lite) {
+        hipLaunchKernelGGL(k_big_label1, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ncand, cand, n, labels,
+                           stop);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const rescore_fn fn = v4 ? k_big_rescore<true, true> : k_big_rescore<false, true>;
+        hipLaunchKernelGGL(fn, dim3(chunks < 4096u ? chunks : 4096u), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
+                           multi, ctl, labels, best, stop);
+    } else {
+        const rescore_fn fn = v4 ? k_big_rescore<true, false> : k_big_rescore<false, false>;
+        hipLaunchKernelGGL(fn, dim3(chunks), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand, (const uint32_t *)nullptr,
+                           ctl, labels, best, stop);
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), (size_t)d * 4, s, X, d, C, k, over, ctl, labels, best,
                        stop);
     return hipGetLastError();

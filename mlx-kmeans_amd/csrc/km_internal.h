@@ -13,7 +13,7 @@ struct km_control {
     int32_t n_empty;     // empty clusters in the last completed pass
     int32_t big;         // first index of the largest count in the last completed pass
     uint32_t n_over;     // rows the wide-row screen listed for a full scan in the running pass
-    int32_t pad1;
+    uint32_t n_multi;    // rows the wide-row screen listed with two or more candidates in the running pass
     double inertia;      // inertia of the last completed pass (of its input centres)
     double prev;         // inertia of the pass before it
     double tol;
@@ -117,11 +117,11 @@ hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, i
                                  uint16_t *Cop, float *maxes, km_control *ctl, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
                                 int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
-                                uint32_t *over, km_control *ctl, const int32_t *stop, hipStream_t s);
+                                uint32_t *over, uint32_t *multi, km_control *ctl, const int32_t *stop, hipStream_t s);
 // lite: the pass returns no per-row distances; single-candidate rows take their label without one
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
-                                 const uint16_t *cand, const uint32_t *over, km_control *ctl, uint32_t *labels,
-                                 float *best, int lite, const int32_t *stop, hipStream_t s);
+                                 const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
+                                 uint32_t *labels, float *best, int lite, const int32_t *stop, hipStream_t s);
 // C_lite non-null: the best column is the rows' FMA-form distances to C, not best[] (pair with a lite rescore)
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
