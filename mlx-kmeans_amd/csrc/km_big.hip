@@ -6,9 +6,9 @@
 //                   1 KB per wave per K-step), and |x|^2 rounded up per row
 //   k_big_centres   per pass: the centres as bf16 MFMA A operands, Cop[chunk][K-step][lane][8], with one extra
 //                   K-step carrying |c|^2 against a B operand of ones; |c| (rounded up) and |c|^2 per centre
-//   k_big_screen    a'_c = |c|^2 - 2 x.c for every (row, centre) on the matrix cores, never stored, twice: the
-//                   first pass finds each row's smallest packed key (value, centre index), the second lists the
-//                   centres inside the error window around it - every centre that can hold the exact minimum
+//   k_big_screen    a'_c = |c|^2 - 2 x.c for every (row, centre) on the matrix cores, never stored, in one pass
+//                   over the centres: the row's smallest packed key (value, centre index) so far, and the centres
+//                   inside the error window around it - every centre that can hold the exact minimum
 //   k_big_rescore   the rows loop (core.py:263-274) on those candidates only, ascending index, strict '<'
 //   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every centre
 //   k_big_hist/scan/scatter/segsum   a stable counting sort of the rows by label and per-cluster sums in row
@@ -16,7 +16,7 @@
 //
 // Labels and best are the rows loop's bit for bit (see the window below). With mode KM_APPROX the screen's
 // minimiser is taken on trust, as the reference's exact=False path does (core.py:878-890, 1061-1088), only its
-// distance is computed exactly, and the screen runs once.
+// distance is computed exactly.
 #pragma clang fp contract(off)
 #include "km_internal.h"
 #include "kmeans_hip.h"
@@ -222,9 +222,10 @@ __global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C
 // plain worst case, and for typical data it is about 2.5 times smaller). The rows loop's float32 direct form s_c satisfies |s_c - D_c| <= g D_c (g = gamma_{D+2}), so a
 // centre can hold the minimum only if a'_c - a'_m <= 2E + 2 g/(1-g) D_m, with D_m <= |x|^2 + a'_m + E for the
 // screen minimiser m. Keys carry the centre index in their low IB mantissa bits (relative perturbation <= RHO),
-// absorbed by the test. Pass A finds the smallest key of each row; pass B recomputes the same screen values
-// (same operands, same instruction sequence, so the same bits) and lists every centre whose key is inside the
-// window. A half-row with more than KB_HALF such centres (or non-finite data) sends the row to a full scan.
+// absorbed by the test. The window only narrows as the row's smallest key falls, so the screen lists, chunk by
+// chunk, every centre inside the window of the smallest key seen so far, prunes a full list against the current
+// window, and at the end keeps the listed centres inside the final window - exactly the centres the final window
+// admits. A half-row with more than KB_HALF of them at once (or non-finite data) sends the row to a full scan.
 
 template <int DS>
 __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
@@ -265,12 +266,11 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     const uint32_t IMASK = (1u << ib) - 1u;
 
     // A operand slices: chunk ch is SPC slices of SLK K-steps (the last possibly shorter), staged through a
-    // two-slice LDS ring; slice g (counted over both passes) is loaded while slice g - 1 is multiplied.
+    // two-slice LDS ring; slice g is loaded while slice g - 1 is multiplied.
     constexpr int SPC = (AK + KB_SLICE - 1) / KB_SLICE;
     constexpr int SLK = (AK + SPC - 1) / SPC;
-    const int passes = approx ? 1 : 2;
     const int GP = nchunks * SPC;
-    const int G = passes * GP;
+    const int G = GP;
     auto issue = [&](int g) {
         char *buf = ring + (g & 1) * (SLK * 1024);
         const int gl = g % GP;
@@ -303,65 +303,82 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
         }
     };
 
-    // ---- pass A: the smallest key of the row
+    const float xsq_up = real_row ? xsq[2 * row] : 0.0f;
+    const float exn = real_row ? xsq[2 * row + 1] : 0.0f;
+    // per-row window terms: T(m) = a + margin(a), a = m + rho |m|, for the row's smallest key m so far. T only
+    // falls as m falls, so a centre kept against an earlier T is a superset of those the final T admits.
+    const float cnmax = maxes[0], csqmax = maxes[1], fmax = maxes[2];
+    const float GDIR = (float)(kb_gamma(d + 2) / (1.0 - kb_gamma(d + 2)) * (1.0 + 0x1p-20));
+    const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
+    const float E = (2.0f * exn * cnmax + nx * fmax + exn * fmax) * (1.0f + 0x1p-20f) + GACC * nx * cnmax +
+                    GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
+    // a key bound Tp with key <= Tp whenever key - rho |key| <= T
+    auto key_bound = [&](float m) {
+        const float akm = m + rho * fabsf(m);
+        const float dm_up = fmaxf(0.0f, xsq_up + akm + E) * (1.0f + 0x1p-20f);
+        float T = akm + ((2.0f * E + 2.0f * GDIR * dm_up) * (1.0f + 0x1p-20f) + TINY);
+        T = T + 0x1p-22f * fabsf(T);
+        float Tp = (T >= 0.0f ? T / (1.0f - rho) : T / (1.0f + rho));
+        Tp = Tp + 0x1p-21f * fabsf(Tp);
+        return (T < INFINITY) ? Tp : -INFINITY;
+    };
+    // One pass over the centre chunks. Per chunk: the row's smallest key so far (both halves), its key bound, and
+    // this chunk's keys inside it appended to this lane's list in LDS (up to KB_HALF; a full list is first pruned
+    // against the current bound, and if still full the row takes the full scan). Approximate mode keeps only the
+    // smallest key.
+    float *list = reinterpret_cast<float *>(ring + 2 * SLK * 1024) + (size_t)wave * KB_HALF * 64 + lane;
     issue(0);
     float m1 = 3.4e38f;
+    int cnt = 0;
+    bool spill = false;
     for (int ch = 0; ch < nchunks; ch++) {
         f32x16 acc;
         screen_chunk(ch * SPC, acc);
+        float key[16];
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
-            m1 = kb_min(m1, kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx));
+            key[v] = kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx);
+            m1 = kb_min(m1, key[v]);
         }
-    }
-    m1 = kb_min(m1, kb_partner(m1, lane));   // both halves of the row
-    const float xsq_up = real_row ? xsq[2 * row] : 0.0f;
-    const float exn = real_row ? xsq[2 * row + 1] : 0.0f;
-    const bool finite = xsq_up < INFINITY && m1 < 3.0e38f;
-    // the window threshold and a key bound Tp with key <= Tp whenever key - rho |key| <= T
-    float T = -INFINITY, Tp = -INFINITY;
-    if (!approx && finite && real_row) {
-        const float cnmax = maxes[0], csqmax = maxes[1], fmax = maxes[2];
-        const float GDIR = (float)(kb_gamma(d + 2) / (1.0 - kb_gamma(d + 2)) * (1.0 + 0x1p-20));
-        const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
-        const float E = (2.0f * exn * cnmax + nx * fmax + exn * fmax) * (1.0f + 0x1p-20f) + GACC * nx * cnmax +
-                        GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
-        const float akm = m1 + rho * fabsf(m1);
-        const float dm_up = fmaxf(0.0f, xsq_up + akm + E) * (1.0f + 0x1p-20f);
-        T = akm + ((2.0f * E + 2.0f * GDIR * dm_up) * (1.0f + 0x1p-20f) + TINY);
-        T = T + 0x1p-22f * fabsf(T);
-        Tp = (T >= 0.0f ? T / (1.0f - rho) : T / (1.0f + rho));
-        Tp = Tp + 0x1p-21f * fabsf(Tp);
-        if (!(T < INFINITY)) Tp = -INFINITY;
-    }
-    // ---- pass B: every centre inside the window; each half-row lane lists at most KB_HALF (more: a full scan)
-    int cnt = 0;
-    bool spill = false;
-    if (!approx) {
-        for (int ch = 0; ch < nchunks; ch++) {
-            f32x16 acc;
-            screen_chunk(GP + ch * SPC, acc);
-            uint64_t any = 0;
-            uint64_t bal[16];
+        if (approx) continue;
+        const float mrow = kb_min(m1, kb_partner(m1, lane));
+        const float Tp = key_bound(mrow);
+        uint64_t bal[16], any = 0;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            bal[v] = __ballot(key[v] <= Tp);
+            any |= bal[v];
+        }
+        if (any) {
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
-                bal[v] = __ballot(kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx) <= Tp);
-                any |= bal[v];
-            }
-            if (any) {   // rare after the first few: some row of the wave has a centre of this chunk in its window
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    if ((bal[v] >> lane) & 1ull) {
-                        const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
-                        if (cnt < KB_HALF && real_row) cand[row * KB_CAP + h * KB_HALF + cnt] = (uint16_t)cidx;
-                        if (cnt >= KB_HALF) spill = true;
-                        cnt++;
+                if ((bal[v] >> lane) & 1ull) {
+                    if (cnt == KB_HALF && !spill) {   // full: drop what the current bound already excludes
+                        int w = 0;
+                        for (int q = 0; q < KB_HALF; q++) {
+                            const float kq = list[q * 64];
+                            if (kq <= Tp) list[(w++) * 64] = kq;
+                        }
+                        cnt = w;
+                        spill = cnt == KB_HALF;
                     }
+                    if (cnt < KB_HALF) list[(cnt++) * 64] = key[v];
                 }
             }
         }
+    }
+    m1 = kb_min(m1, kb_partner(m1, lane));   // both halves of the row
+    const bool finite = xsq_up < INFINITY && m1 < 3.0e38f;
+    if (!approx && finite && real_row) {
+        // the final bound: keep the listed centres inside it
+        const float Tp = key_bound(m1);
+        int w = 0;
+        for (int q = 0; q < cnt; q++) {
+            const float kq = list[q * 64];
+            if (kq <= Tp) cand[row * KB_CAP + h * KB_HALF + (w++)] = (uint16_t)(kb_u32(kq) & IMASK);
+        }
+        cnt = w;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (!real_row) return;
@@ -920,7 +937,8 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
     if (!fn) return hipErrorInvalidValue;
     const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
     const unsigned blocks = (unsigned)((pl.ntiles + KB_WAVES - 1) / KB_WAVES);
-    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), 2 * KB_SLICE * 1024, s, X16T, xsq, n, d, Cop, maxes, k,
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), 2 * KB_SLICE * 1024 + KB_WAVES * KB_HALF * 64 * 4, s, X16T,
+                       xsq, n, d, Cop, maxes, k,
                        pl.nchunks, pl.ib, rho, mode == KM_APPROX ? 1 : 0, ncand, cand, over, multi, ctl, stop);
     return hipGetLastError();
 }
