@@ -376,35 +376,24 @@ __global__ __launch_bounds__(256) void k_finish(const double *__restrict__ tmp, 
                                                 double *__restrict__ tot, float *__restrict__ Cnext, int flags,
                                                 const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
-    const int c = blockIdx.x, tid = threadIdx.x, W = d + 2;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int c = blockIdx.x, W = d + 2;
     const int64_t kw = (int64_t)k * W;
-    __shared__ double s_cnt;
-    // entry j of this cluster = the sum of its S range sums, lane s taking range s (S <= 64) and a fixed
-    // butterfly adding them; wave w takes entries w, w + 4, ...; the count (entry 0) first
+    // entry j of this cluster = its S range sums added in ascending order by thread j (and every thread adds the
+    // count's own, the same way, to divide by it)
     const double *src = tmp + (int64_t)c * W;
-    if (wave == 0) {
-        double v = lane < S ? src[(int64_t)lane * kw] : 0.0;
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) {
-            tot[(int64_t)c * W] = v;
-            s_cnt = v;
-        }
-    }
-    __syncthreads();
-    const long long cnt = llrint(s_cnt);
+    double cntd = 0.0;
+    for (int sp = 0; sp < S; sp++) cntd += src[(int64_t)sp * kw];
+    const long long cnt = llrint(cntd);
     const bool update = (flags & KM_FIN_UPDATE) != 0;
-    for (int j = 1 + wave; j < W; j += 4) {
-        double v = lane < S ? src[(int64_t)lane * kw + j] : 0.0;
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) {
-            tot[(int64_t)c * W + j] = v;
-            if (update && j >= 2 && cnt > 0) Cnext[(int64_t)c * d + (j - 2)] = (float)(v / (double)cnt);
-        }
+    for (int j = threadIdx.x; j < W; j += 256) {
+        double v = 0.0;
+        for (int sp = 0; sp < S; sp++) v += src[(int64_t)sp * kw + j];
+        tot[(int64_t)c * W + j] = v;
+        if (update && j >= 2 && cnt > 0) Cnext[(int64_t)c * d + (j - 2)] = (float)(v / (double)cnt);
     }
     if (update && (flags & KM_FIN_SPHERICAL) && cnt > 0) {
         __syncthreads();
-        if (wave == 0) normalise_row(Cnext, c, d, lane);
+        if (threadIdx.x < 64) normalise_row(Cnext, c, d, threadIdx.x);
     }
 }
 
