@@ -200,6 +200,36 @@ def test_screen_edge_cases_match_the_rows_loop(lib, d, k):
     ctx.close()
 
 
+@pytest.mark.parametrize("d,k", [(48, 100), (96, 40)])
+def test_wide_rows_over_slices(lib, d, k):
+    """The wide-row path over three uneven slices: a pass with per-row outputs is the oracle's bit for bit; Lloyd
+    steps without them (single-candidate rows unscored, multi-candidate rows listed per slice) match the oracle's
+    centres, inertia and empty counts; three steps in a row keep matching."""
+    import oracle
+    rng = np.random.default_rng(41 + d + k)
+    n = 50_000
+    cen = rng.uniform(-2, 2, size=(k // 2, d)).astype(np.float32)
+    X = (cen[rng.integers(0, len(cen), n)] + 0.7 * rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(n, k, replace=False)].copy()
+    parts = [X[:17_003], X[17_003:17_100], X[17_100:]]
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    say(f"[gpu] wide rows over slices d={d} k={k}")
+    tot, labels, best = ctx.run_pass(C, labels=True, best=True)
+    assert ctx.last_path() == "mfma"
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(labels, ol) and np.array_equal(best.view(np.uint32), ob.view(np.uint32))
+    for s in range(3):
+        C_new, inertia, n_empty = ctx.lloyd_step(C)
+        R_new, r_in, r_empty, _, _, _ = oracle.lloyd_step(X, C)
+        assert n_empty == r_empty
+        assert abs(inertia - r_in) <= INERTIA_TOL * r_in
+        assert float(np.max(np.abs(C_new.astype(np.float64) - R_new.astype(np.float64)))) / scale <= CENTRE_TOL
+        C = R_new
+    ctx.close()
+
+
 @pytest.mark.parametrize("name", ["outliers_d32", "lowd_d8", "pixels_d4"])
 def test_reruns_are_bit_identical(lib, name):
     parts, C0, _ = G.case_inputs(name)
