@@ -13,7 +13,9 @@
  * Exactness contract (mode KM_EXACT): every label is the centre with the smallest float32 distance
  * s = sum_j (x_j - c_j)^2, accumulated for j ascending with the product and the add rounded separately,
  * lowest index on an exact tie (the rows loop, core.py:263-274); best is that s. Whatever kernel path runs,
- * the labels and best values are these, bit for bit.
+ * the labels and best values are these, bit for bit. Mode KM_APPROX (exact=False, estimator.py:18-30): on the
+ * wide-row path (16 < dims <= 768, k <= 4096, k * dims >= 1024) the label is the bf16 screen's minimiser, taken on
+ * trust, and best is the exact distance above to that label; every other path is exact in either mode.
  */
 #ifndef KMEANS_HIP_H
 #define KMEANS_HIP_H
@@ -85,8 +87,8 @@ int32_t km_lloyd_step(km_ctx *ctx, const float *C, int32_t k, int32_t mode, int3
                       double *inertia, int32_t *n_empty);
 
 /* Up to max_iter Lloyd iterations from C0 (host, k x dims) with the reference's stopping rule
- * |prev - inertia| <= tol * prev (estimator.py:147-149; a negative tol never stops a loop with inertia > 0), spherical renormalisation when spherical != 0
- * (estimator.py:127-130, 141-142). Iterations run back to back on the device; the host looks at the
+ * |prev - inertia| <= tol * prev (estimator.py:147-149; a negative tol never stops a loop with inertia > 0),
+ * spherical renormalisation when spherical != 0 (estimator.py:127-130, 141-142). Iterations run back to back on the device; the host looks at the
  * device-side state only every few iterations and when a cluster empties. Outputs (host): C_out the final
  * centres, *last_inertia the inertia reported by the last iteration, *n_iter the iterations run,
  * *n_relocated the total empty clusters relocated. Replaces KMeans._one_run's loop (estimator.py:132-150). */
@@ -101,8 +103,10 @@ int32_t km_profile_read(km_ctx *ctx, int32_t kernel, double *ms_total, int64_t *
 const char *km_kernel_name(int32_t kernel);
 
 /* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS, _MFMA or _FUSED), and the number of
- * rows in that pass that the MFMA screen could not settle alone: rows with more than one centre inside the
- * screen's error window, each rescored with the direct form against every centre in its window. */
+ * rows in that pass the matrix-core screen could not settle with its candidate list: on the fused path (dims 16,
+ * 32, 64) rows with more than one centre inside the error window, rescored against every centre in it; on the
+ * wide-row path rows that took the full scan of every centre (more than 16 centres in a half-row's window, or
+ * non-finite data). 0 on the other paths. */
 int32_t km_last_path(const km_ctx *ctx);
 int64_t km_last_fallback_rows(km_ctx *ctx);
 

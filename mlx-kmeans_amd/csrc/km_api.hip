@@ -312,7 +312,7 @@ static bool big_ok(const km_ctx *c, int k) {
 // Returns the kernel family for this pass (FAM_*), or -1 when an explicit path does not serve the shape.
 static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
     const bool al = parts_aligned(c);
-    *mp = km_plan_mfma(c->n, c->d, k, 1);
+    *mp = km_plan_mfma(c->n, c->d, k);
     if (!al) mp->ok = 0;
     const bool lowd_ok = km_plan_lowd(c->n, c->d, k, al).ok != 0;
     const bool wide_ok = big_ok(c, k);
@@ -330,7 +330,7 @@ static int32_t family_path(int fam) {
 }
 
 // Sizes the per-pass workspaces. Returns KM_OK or an error.
-static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bool need_rows_scratch) {
+static int ensure_pass_buffers(km_ctx *c, int k, size_t total_rb, bool need_rows_scratch) {
     const int64_t kw = (int64_t)k * (c->d + 2);
     HIPCHK(c, c->psum.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)kw));
@@ -340,7 +340,6 @@ static int ensure_pass_buffers(km_ctx *c, int k, int chosen, size_t total_rb, bo
         HIPCHK(c, c->labels.ensure((size_t)c->n));
         HIPCHK(c, c->best.ensure((size_t)c->n));
     }
-    (void)chosen;
     return KM_OK;
 }
 
@@ -441,7 +440,6 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
 // device arrays of n (or null) for the per-row results. gated: every kernel checks ctl->stop first.
 static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, float *best_d, bool gated, int pass,
                     double tol, int flags) {
-    (void)mode;
     HIPCHK(c, c->Cb[(pass + 1) & 1].ensure((size_t)k * c->d));
     const float *Cin = c->Cb[pass & 1].p;
     km_mfma_plan mp;
@@ -451,7 +449,6 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
                     path == KM_PATH_MFMA ? "mfma" : "fused", k, c->d);
     c->last_path = family_path(fam);
     c->last_family = fam;
-    const int chosen = c->last_path;
     const int32_t *stop = gated ? &c->ctl->stop : nullptr;
     const int d = c->d;
 
@@ -463,10 +460,10 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         size_t total_rb = 0;
         std::vector<km_mfma_plan> plans;
         for (auto &p : c->parts) {
-            plans.push_back(km_plan_mfma(p.rows, d, k, 1));
+            plans.push_back(km_plan_mfma(p.rows, d, k));
             total_rb += plans.back().nrb;
         }
-        int r = ensure_pass_buffers(c, k, chosen, total_rb, false);
+        int r = ensure_pass_buffers(c, k, total_rb, false);
         if (r) return r;
         int rb = 0;
         int64_t row0 = 0;
@@ -492,7 +489,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             plans.push_back(km_plan_lowd(p.rows, d, k, al));
             total_rb += plans.back().nrb;
         }
-        int r = ensure_pass_buffers(c, k, chosen, total_rb, false);
+        int r = ensure_pass_buffers(c, k, total_rb, false);
         if (r) return r;
         int rb = 0;
         int64_t row0 = 0;
@@ -500,7 +497,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             const Part &p = c->parts[i];
             uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
             float *bst = best_d ? best_d + row0 : nullptr;
-            HIPCHK(c, launch(c, KK_FUSED_ROWS, [&] {
+            HIPCHK(c, launch(c, KK_FUSED_LOWD, [&] {
                 return km_launch_lowd(plans[i], p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p, rb, stop,
                                       c->stream);
             }));
@@ -517,7 +514,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         plans.push_back(km_plan_accum_generic(p.rows, d, k));
         total_rb += plans.back().nrb;
     }
-    int r = ensure_pass_buffers(c, k, chosen, total_rb, true);
+    int r = ensure_pass_buffers(c, k, total_rb, true);
     if (r) return r;
     uint32_t *lab_all = labels_d ? labels_d : c->labels.p;
     float *best_all = best_d ? best_d : c->best.p;

@@ -27,7 +27,7 @@ enum km_kernel_id {
     KK_REDUCE,
     KK_FINISH,
     KK_NORMALISE,
-    KK_FUSED_ROWS,
+    KK_FUSED_LOWD,
     KK_FUSED_MFMA,
     KK_BIG_PREP,
     KK_BIG_SCREEN,
@@ -77,7 +77,7 @@ struct km_mfma_plan {
     int waves;       // waves per block
     size_t lds;
 };
-km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused);
+km_mfma_plan km_plan_mfma(int64_t n, int d, int k);
 // want_best: every row's exact direct-form distance (labels/best outputs); without it, rows the screen settles
 // alone add an FMA-form distance to the pass inertia (their labels are exact either way).
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,

@@ -777,8 +777,7 @@ static const fused_entry *find_fused(int d, int k) {
 static int g_cus = 0;
 static size_t g_lds_max = 0;
 
-km_mfma_plan km_plan_mfma(int64_t n, int d, int k, int fused) {
-    (void)fused;
+km_mfma_plan km_plan_mfma(int64_t n, int d, int k) {
     km_mfma_plan pl{};
     const fused_entry *fe = find_fused(d, k);
     if (!fe || n < 1) return pl;
