@@ -24,8 +24,6 @@
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void *lds_vptr;
-typedef __attribute__((address_space(1))) void *gbl_vptr;
 
 static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
 static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row

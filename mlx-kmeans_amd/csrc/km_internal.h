@@ -3,6 +3,29 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+typedef __attribute__((address_space(3))) void *lds_vptr;
+typedef __attribute__((address_space(1))) void *gbl_vptr;
+
+// Direct global->LDS load of 16 bytes per lane (global_load_lds_dwordx4: lane i's bytes land at dst + 16 i). It is
+// issued from inline assembly so that the compiler neither tracks it nor waits for it: the caller's own
+// s_waitcnt vmcnt(n) says when the data is in LDS. (Through the builtin, the compiler may wait for every pending
+// direct load before the next LDS access of any kind: in the fused kernel's loop it did, before the first read of
+// the current block, which drained the double buffer at every step.) M0 holds the
+// wave-uniform LDS address and needs one wait state before the load reads it. M0 is a register the compiler
+// reserves (it sets it before each of its own uses), so naming it as clobbered is harmless and only warned about.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void *src, lds_vptr dst) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+// The same for 4 bytes per lane (global_load_lds_dword: lane i's word lands at dst + 4 i).
+__device__ __forceinline__ void lds_dma4(const void *src, lds_vptr dst) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Device-resident state of a fit loop. One per context; the update kernels read and write it so that
 // iterations can run back to back with no host round trip.
 struct km_control {
@@ -68,11 +91,12 @@ hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot,
                             int pass, double tol, int flags, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_normalise(float *C, int k, int d, hipStream_t s);
 
-// MFMA-screened exact assignment. Fused variant also accumulates into partials (one row-block per block).
+// MFMA-screened exact assignment. Fused variant also accumulates into partials (one per workgroup, which takes
+// blocks of 64 rows per wave round-robin).
 struct km_mfma_plan {
     int ok;          // 0 if the shape is not served
     int kpad, dpad;  // padded centre count and dims
-    int64_t rbs;     // rows per block (fused)
+    int64_t rbs;     // at most this many rows per workgroup (fused)
     int nrb;         // blocks
     int waves;       // waves per block
     size_t lds;

@@ -241,8 +241,12 @@ struct Lay {
     static constexpr int BUF = 2 * QI * RB;   // bytes per 64-row block
 };
 
-typedef __attribute__((address_space(3))) void *lds_vptr;
-typedef __attribute__((address_space(1))) void *gbl_vptr;
+
+// wait until at most N vector memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // issue the loads of the 64-row block starting at r0 (rows past r_end read row r_end - 1; never used)
 template <int D>
@@ -258,7 +262,7 @@ __device__ __forceinline__ void issue_block(const float *__restrict__ X, int64_t
 #pragma unroll
         for (int q = 0; q < L::QI; q++) {
             const float *src = X + row * D + 4 * (h * L::QI + q);
-            __builtin_amdgcn_global_load_lds((gbl_vptr)src, (lds_vptr)(buf + (tile * L::QI + q) * L::RB), 16, 0, 0);
+            lds_dma16(src, (lds_vptr)(buf + (tile * L::QI + q) * L::RB));
         }
     }
 }
@@ -291,7 +295,7 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
 
 template <int D, int KP, int WAVES, bool ACCUM, bool BEST>
 __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
-    const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k, int64_t rbs,
+    const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k,
     uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
     int rb0, km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
     using G = Geo<D, KP>;
@@ -330,9 +334,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * L::BUF);   // labels of the block (0x4000: no row)
     uint32_t *CNT = reinterpret_cast<uint32_t *>(wbase + WBYTES - 4 * KP);   // rows per centre (this wave)
 
-    const int64_t r_begin = (int64_t)blockIdx.x * rbs;
-    const int64_t r_end = (r_begin + rbs < n) ? r_begin + rbs : n;
-    int64_t r0 = r_begin + (int64_t)wave * 64;
+    // blocks of 64 WAVES rows go round-robin to the workgroups (at any time the whole grid streams one window of
+    // the rows), 64 rows per wave
+    const int64_t r_end = n, step = (int64_t)gridDim.x * 64 * WAVES;
+    int64_t r0 = (int64_t)blockIdx.x * 64 * WAVES + (int64_t)wave * 64;
     if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, wbase);
 
     for (int e = threadIdx.x; e < KP * CS; e += 64 * WAVES) {
@@ -399,17 +404,15 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 
     // the two block buffers alternate by offset (pointer arithmetic keeps the LDS address space visible)
     int cur = 0;
-    for (; r0 < r_end; r0 += 64 * WAVES, cur ^= L::BUF) {
+    for (; r0 < r_end; r0 += step, cur ^= L::BUF) {
         const char *buf = wbase + cur;
         // ---- prefetch the next block into the other buffer, then wait for this one
-        const int64_t r1 = r0 + 64 * WAVES;
+        const int64_t r1 = r0 + step;
         if (r1 < r_end) {
             issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ L::BUF));
-            if (L::QI == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-            else if (L::QI == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+            vm_wait<2 * L::QI>();
         } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            vm_wait<0>();
         }
         const int64_t row = r0 + lane;     // the row this lane owns after the exchange
         const bool valid = row < r_end;
@@ -740,7 +743,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 
 // ------------------------------------------------------------------ planning and launch
 
-typedef void (*fused_fn)(const float *, int64_t, const float *, int, int64_t, uint32_t *, float *, float *, float *,
+typedef void (*fused_fn)(const float *, int64_t, const float *, int, uint32_t *, float *, float *, float *,
                          int, km_control *, const int32_t *);
 
 // One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
@@ -817,10 +820,8 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k) {
     const int64_t units = (n + unit - 1) / unit;
     int64_t nrb = units < slots ? units : slots;
     if (nrb < 1) nrb = 1;
-    int64_t rbs = (n + nrb - 1) / nrb;
-    rbs = (rbs + unit - 1) / unit * unit;
-    pl.rbs = rbs;
-    pl.nrb = (int)((n + rbs - 1) / rbs);
+    pl.nrb = (int)nrb;
+    pl.rbs = (units + nrb - 1) / nrb * unit;   // at most this many rows per block
     return pl;
 }
 
@@ -830,7 +831,7 @@ hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X,
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
     fused_fn fn = pl.waves == 4 ? (want_best ? fe->acc4b : fe->acc4) : (want_best ? fe->acc2b : fe->acc2);
-    hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, pl.rbs, labels, best, psum,
+    hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, labels, best, psum,
                        pcomp, rb0, ctl, stop);
     return hipGetLastError();
 }
