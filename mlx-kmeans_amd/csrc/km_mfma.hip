@@ -59,6 +59,12 @@ __device__ __forceinline__ float vmin(float a, float b) {
     asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
+// v_min3_f32, defined as two v_min_f32 in a row (the same result for every input, NaN included)
+__device__ __forceinline__ float vmin3(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 __device__ __forceinline__ float f32(uint32_t v) { return __uint_as_float(v); }
 
 // v_permlane32_swap: lane l < 32 gets (va of lane l, va of lane l+32); lane l >= 32 gets (vb of lane l-32,
@@ -145,13 +151,16 @@ __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], flo
     constexpr uint32_t IMASK = (1u << G::IB) - 1u;
     m1 = 3.4e38f;
     m2 = 3.4e38f;
+    // two keys at a time: the smallest of {m1, m2, a, b} is min3(m1, a, b) (m1 <= m2), the second the smaller of
+    // m2 and the middle of (m1, a, b): three instructions per pair instead of four
 #pragma unroll
     for (int t = 0; t < G::KT; t++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const float key = f32((u32(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
-            m2 = __builtin_amdgcn_fmed3f(m1, m2, key);
-            m1 = vmin(m1, key);
+        for (int v = 0; v < 16; v += 2) {
+            const float ka = f32((u32(a[t][v]) & ~IMASK) | (uint32_t)(t * 16 + v));
+            const float kb = f32((u32(a[t][v + 1]) & ~IMASK) | (uint32_t)(t * 16 + v + 1));
+            m2 = vmin(m2, __builtin_amdgcn_fmed3f(m1, ka, kb));
+            m1 = vmin3(m1, ka, kb);
         }
 }
 
@@ -228,19 +237,24 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8 &ph, bf16x8 &
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Rows reach LDS by direct global->LDS loads (global_load_lds_dwordx4), double-buffered one 64-row block
-// ahead. A block is two 32-row tiles; a tile of D floats per row is NC = D/4 16-byte chunks per row, loaded
-// by NC/2 instructions: instruction q puts chunk q of row ln in lane ln (lanes 0-31) and chunk NC/2+q of row
-// (ln ^ 4) in lane 32+ln. Instruction regions are 1040 bytes apart (1024 + a 16-byte pad). With this layout the
-// screen's half-row reads and the accumulation's transposed reads (one dim, eight rows per lane) both touch
-// distinct LDS banks.
+// ahead. A block is its 64 rows in order (D floats = NC 16-byte chunks each); one load instruction moves 1 KB, i.e.
+// 64/NC whole rows read contiguously, lane i taking the 16 bytes that land at LDS offset 16 i. Within each row the
+// chunks are permuted (chunk c of block row r sits at position c ^ swz(r)) so that the screen's half-row reads
+// (eight lanes on eight consecutive rows, one chunk each) and the accumulation's transposed reads (one dim per
+// lane, one row per read) touch distinct LDS banks (32 banks of 4 bytes). swz depends only on the row's low bits,
+// which are compile-time in the transposed reads, so their addresses stay a few registers plus immediates.
 template <int D>
 struct Lay {
-    static constexpr int NC = D / 4;          // 16-byte chunks per row
-    static constexpr int QI = NC / 2;         // load instructions per tile
-    static constexpr int RB = 1040;           // bytes per instruction region
-    static constexpr int BUF = 2 * QI * RB;   // bytes per 64-row block
+    static constexpr int NC = D / 4;           // 16-byte chunks per row
+    static constexpr int QI = NC / 2;          // chunks per half row (the screen's reads per tile)
+    static constexpr int RPI = 64 / NC;        // rows per load instruction
+    static constexpr int BUF = 64 * D * 4;     // bytes per 64-row block (NC instructions)
 };
 
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+    return D == 16 ? ((r >> 1) & 3) : (r & 7);
+}
 
 // wait until at most N vector memory operations of this wave are outstanding
 template <int N>
@@ -253,18 +267,44 @@ template <int D>
 __device__ __forceinline__ void issue_block(const float *__restrict__ X, int64_t r0, int64_t r_end, int lane,
                                             char *buf) {
     using L = Lay<D>;
-    const int ln = lane & 31, h = lane >> 5;
+    const int p = lane % L::NC;   // this lane's position within its row
 #pragma unroll
-    for (int tile = 0; tile < 2; tile++) {
-        const int rr = h ? (ln ^ 4) : ln;
-        int64_t row = r0 + 32 * tile + rr;
+    for (int q = 0; q < L::NC; q++) {
+        const int r = q * L::RPI + lane / L::NC;   // block row
+        int64_t row = r0 + r;
         row = row < r_end ? row : r_end - 1;
-#pragma unroll
-        for (int q = 0; q < L::QI; q++) {
-            const float *src = X + row * D + 4 * (h * L::QI + q);
-            lds_dma16(src, (lds_vptr)(buf + (tile * L::QI + q) * L::RB));
-        }
+        const float *src = X + row * D + 4 * (p ^ swz<D>(r));
+        lds_dma16(src, (lds_vptr)(buf + q * 1024));
     }
+}
+
+// The same for a block wholly inside the rows: the block's first row as a scalar base, this lane's byte offset
+// into instruction q's kilobyte (voff0 for even q, voff1 for odd: they differ only at D = 64) and q * 1024 as
+// immediates, so issuing takes no vector instructions.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // M0 in the clobbers: see lds_dma16
+template <int D, int Q>
+__device__ __forceinline__ void issue_block_inner(const char *blk, uint32_t voff0, uint32_t voff1, uint32_t mb) {
+    if constexpr (Q < Lay<D>::NC) {
+        const char *sb = blk + (Q / 4) * 4096;   // the immediate offset reaches 4095
+        asm volatile("s_add_u32 m0, %1, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2 offset:%3"
+                     ::"v"((Q & 1) ? voff1 : voff0), "s"(mb), "s"(sb), "n"((Q % 4) * 1024), "n"(Q * 1024)
+                     : "memory", "m0", "scc");
+        issue_block_inner<D, Q + 1>(blk, voff0, voff1, mb);
+    }
+}
+#pragma clang diagnostic pop
+template <int D>
+__device__ __forceinline__ void issue_block_inner_all(const float *blk, uint32_t voff0, uint32_t voff1, char *buf) {
+    const uint32_t mb = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_vptr)buf);
+    issue_block_inner<D, 0>(reinterpret_cast<const char *>(blk), voff0, voff1, mb);
+}
+// this lane's byte offset into the kilobyte of load instruction q (see issue_block)
+template <int D>
+__device__ __forceinline__ uint32_t issue_voff(int lane, int q) {
+    using L = Lay<D>;
+    const int r = q * L::RPI + lane / L::NC;
+    return (uint32_t)((lane / L::NC) * D * 4 + 16 * ((lane % L::NC) ^ swz<D>(r)));
 }
 
 // this lane's half row of tile `tile` (row ln, dims h*D/2 ..) from a loaded block
@@ -272,10 +312,11 @@ template <int D>
 __device__ __forceinline__ void read_half(const char *buf, int tile, int lane, float (&x)[D / 2]) {
     using L = Lay<D>;
     const int ln = lane & 31, h = lane >> 5;
-    const int slot = h ? 32 + (ln ^ 4) : ln;
+    const int r = 32 * tile + ln, sw = swz<D>(r);
+    const char *row = buf + r * (D * 4);
 #pragma unroll
     for (int q = 0; q < L::QI; q++) {
-        const float4 v = *reinterpret_cast<const float4 *>(buf + (tile * L::QI + q) * L::RB + slot * 16);
+        const float4 v = *reinterpret_cast<const float4 *>(row + ((h * L::QI + q) ^ sw) * 16);
         x[4 * q] = v.x;
         x[4 * q + 1] = v.y;
         x[4 * q + 2] = v.z;
@@ -286,11 +327,7 @@ __device__ __forceinline__ void read_half(const char *buf, int tile, int lane, f
 // x[row][dim] of a loaded block (row < 64, dim < D)
 template <int D>
 __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
-    using L = Lay<D>;
-    const int tile = row >> 5, rr = row & 31, c = dim >> 2;
-    const int hp = c >= L::QI, q = hp ? c - L::QI : c;
-    const int slot = hp ? 32 + (rr ^ 4) : rr;
-    return *reinterpret_cast<const float *>(buf + (tile * L::QI + q) * L::RB + slot * 16 + (dim & 3) * 4);
+    return *reinterpret_cast<const float *>(buf + row * (D * 4) + (((dim >> 2) ^ swz<D>(row)) * 16) + (dim & 3) * 4);
 }
 
 template <int D, int KP, int WAVES, bool ACCUM, bool BEST>
@@ -338,7 +375,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     // the rows), 64 rows per wave
     const int64_t r_end = n, step = (int64_t)gridDim.x * 64 * WAVES;
     int64_t r0 = (int64_t)blockIdx.x * 64 * WAVES + (int64_t)wave * 64;
-    if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, wbase);
+    const uint32_t voff0 = issue_voff<D>(lane, 0), voff1 = issue_voff<D>(lane, 1);
+    if (r0 + 64 <= r_end) issue_block_inner_all<D>(X + r0 * D, voff0, voff1, wbase);
+    else if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, wbase);
 
     for (int e = threadIdx.x; e < KP * CS; e += 64 * WAVES) {
         const int c = e / CS, j = e % CS;
@@ -409,8 +448,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         // ---- prefetch the next block into the other buffer, then wait for this one
         const int64_t r1 = r0 + step;
         if (r1 < r_end) {
-            issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ L::BUF));
-            vm_wait<2 * L::QI>();
+            if (r1 + 64 <= r_end) issue_block_inner_all<D>(X + r1 * D, voff0, voff1, wbase + (cur ^ L::BUF));
+            else issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ L::BUF));
+            vm_wait<L::NC>();
         } else {
             vm_wait<0>();
         }
@@ -765,7 +805,7 @@ static fused_entry g_fused[] = {
 
 // mirrors the kernel's layout: centres, then per wave max(two block buffers + labels + counts, fold + counts)
 static size_t lds_for(int d, int kp, int waves) {
-    const size_t loop = 2 * (size_t)(2 * (d / 8) * 1040) + 128 + 4 * (size_t)kp;
+    const size_t loop = 2 * (size_t)(64 * d * 4) + 128 + 4 * (size_t)kp;
     const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float) + 4 * (size_t)kp;
     return (size_t)kp * (d + 1) * sizeof(float) + waves * (loop > fold ? loop : fold);
 }
