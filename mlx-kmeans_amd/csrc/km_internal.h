@@ -19,11 +19,6 @@ __device__ __forceinline__ void lds_dma16(const void *src, lds_vptr dst) {
     const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
-// The same for 4 bytes per lane (global_load_lds_dword: lane i's word lands at dst + 4 i).
-__device__ __forceinline__ void lds_dma4(const void *src, lds_vptr dst) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
-}
 #pragma clang diagnostic pop
 
 // Device-resident state of a fit loop. One per context; the update kernels read and write it so that

@@ -279,8 +279,9 @@ __device__ __forceinline__ void issue_block(const float *__restrict__ X, int64_t
 }
 
 // The same for a block wholly inside the rows: the block's first row as a scalar base, this lane's byte offset
-// into instruction q's kilobyte (voff0 for even q, voff1 for odd: they differ only at D = 64) and q * 1024 as
-// immediates, so issuing takes no vector instructions.
+// into instruction q's kilobyte (voff0 for even q, voff1 for odd: they differ only at D = 64) and immediates, so
+// issuing takes no vector instructions. The instruction's immediate offset moves the LDS address as well as the
+// global one, so M0 carries only the part of q * 1024 the immediate does not.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"   // M0 in the clobbers: see lds_dma16
 template <int D, int Q>
@@ -288,7 +289,7 @@ __device__ __forceinline__ void issue_block_inner(const char *blk, uint32_t voff
     if constexpr (Q < Lay<D>::NC) {
         const char *sb = blk + (Q / 4) * 4096;   // the immediate offset reaches 4095
         asm volatile("s_add_u32 m0, %1, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2 offset:%3"
-                     ::"v"((Q & 1) ? voff1 : voff0), "s"(mb), "s"(sb), "n"((Q % 4) * 1024), "n"(Q * 1024)
+                     ::"v"((Q & 1) ? voff1 : voff0), "s"(mb), "s"(sb), "n"((Q % 4) * 1024), "n"((Q / 4) * 4096)
                      : "memory", "m0", "scc");
         issue_block_inner<D, Q + 1>(blk, voff0, voff1, mb);
     }
