@@ -74,6 +74,29 @@ def cpu_baseline(X, C, budget_s=12.0):
                       f"kmeans.mm CPU backend restated (oracle/kmeans_oracle.c orc_cpu_pass)"}
 
 
+def seed_probe(workload):
+    """k-means++ seeding time at the workload's shape: the GPU seeding KMeans.fit uses, against the host float64
+    greedy k-means++ the synthetic workloads use for their start centres (same sample size and trials)."""
+    import torch
+    from mlx_kmeans import core, synthetic
+    w = synthetic.WORKLOADS[workload]()
+    X, k = w["X"], w["k"]
+    n = len(X)
+    dd = core.DeviceData([X])
+    core.kmeans_pp_init(dd, n, k, np.random.default_rng(1))   # warm
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    core.kmeans_pp_init(dd, n, k, np.random.default_rng(1))
+    gpu_ms = (time.perf_counter() - t0) * 1e3
+    dd.close()
+    t0 = time.perf_counter()
+    synthetic.kmeans_pp_init([X], n, k, np.random.default_rng(1))
+    host_ms = (time.perf_counter() - t0) * 1e3
+    m = min(n, min(200_000, max(20_000, 20 * k)))
+    print(json.dumps({"seed_probe": workload, "k": k, "dims": X.shape[1], "sample_rows": m, "gpu_ms": round(gpu_ms, 2),
+                      "host_f64_ms": round(host_ms, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -83,6 +106,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--approx", action="store_true",
                     help="exact=False: the wide-row screen's minimiser taken on trust (other shapes run exact)")
+    ap.add_argument("--seed-probe", action="store_true",
+                    help="only time k-means++ seeding of the workload (GPU, and the host float64 version)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB with torch (a plain copy kernel of known size, for counter calibration)")
     a = ap.parse_args()
@@ -94,6 +119,9 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": x.numel() * 4}), flush=True)
+        return
+    if a.seed_probe:
+        seed_probe(a.workload)
         return
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {a.gpus} is not supported (the Lloyd pass shards by rows; "

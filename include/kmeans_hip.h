@@ -95,6 +95,17 @@ int32_t km_lloyd_step(km_ctx *ctx, const float *C, int32_t k, int32_t mode, int3
 int32_t km_fit(km_ctx *ctx, const float *C0, int32_t k, int32_t max_iter, double tol, int32_t mode,
                int32_t spherical, float *C_out, double *last_inertia, int32_t *n_iter, int32_t *n_relocated);
 
+/* Greedy k-means++ seeding on a sample of the rows, every round on the device (replaces kmeans_pp_init,
+ * core.py:153-192, and its kernels core.py:70-106). sample: m ascending global row indices (host; the reference
+ * draws them with rng.choice(rows, m, replace=False), sorted); first: the first pick, an index into the sample;
+ * seeds: k - 1 per-round seeds (host; the reference's rng.integers(2**63 - 1, size=k - 1)). Round r keeps, of
+ * 2 + floor(ln k) candidates drawn with probability proportional to the squared distance to the nearest pick so
+ * far (candidate t: the row with the largest d2 / (-ln u), u from splitmix64(seed_r ^ splitmix64(i * trials + t))),
+ * the one that lowers the summed squared distance the most (first on a tie). C_out (host, k x dims): the picked
+ * rows in pick order. Requires m >= k and 2 + floor(ln k) <= 16. */
+int32_t km_seed_pp(km_ctx *ctx, int32_t k, const int64_t *sample, int64_t m, int64_t first, const uint64_t *seeds,
+                   float *C_out);
+
 /* Kernel timing with HIP events on the context's stream. km_profile(ctx, 1) clears and starts recording;
  * km_profile_read gives, for kernel id `kernel`, the summed milliseconds and launch count so far.
  * km_kernel_name(id) names an id ("" past the last); ids are stable within one build. */

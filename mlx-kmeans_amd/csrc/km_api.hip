@@ -85,6 +85,9 @@ struct km_ctx {
     DBuf<double> red;       // range sums of the reduce (S, k * (d + 2))
     DBuf<uint32_t> labels;
     DBuf<float> best;
+    DBuf<float> pp_S, pp_C;     // k-means++: the row sample (transposed, dims x m) and the picked rows
+    DBuf<int64_t> pp_idx;       // k-means++: the sample's row indices, local to their slice
+    DBuf<char> pp_ws;           // k-means++: the rounds' workspace
     km_control *ctl = nullptr;    // device
     km_control *ctl_h = nullptr;  // pinned host mirror
     bool prof = false;
@@ -211,6 +214,10 @@ extern "C" void km_destroy(km_ctx *c) {
     c->red.release();
     c->labels.release();
     c->best.release();
+    c->pp_S.release();
+    c->pp_C.release();
+    c->pp_idx.release();
+    c->pp_ws.release();
     for (auto &r : c->recs) {
         (void)hipEventDestroy(r.a);
         (void)hipEventDestroy(r.b);
@@ -768,6 +775,55 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     if (last_inertia) *last_inertia = c->ctl_h->inertia;
     if (n_iter) *n_iter = c->ctl_h->iter;
     if (n_relocated) *n_relocated = relocated;
+    harvest(c);
+    return KM_OK;
+}
+
+// ------------------------------------------------------------------ k-means++ seeding
+
+extern "C" int32_t km_seed_pp(km_ctx *c, int32_t k, const int64_t *sample, int64_t m, int64_t first,
+                              const uint64_t *seeds, float *C_out) {
+    if (!c) return KM_EINVAL;
+    if (c->n == 0) return fail(c, KM_ENODATA, "no data set on the context");
+    if (k < 1) return fail(c, KM_EINVAL, "n_clusters must be a positive integer");
+    if (!sample || !C_out || (k > 1 && !seeds)) return fail(c, KM_EINVAL, "sample, seeds and C_out must not be null");
+    if (m < k) return fail(c, KM_EINVAL, "n_samples=%lld should be >= n_clusters=%d", (long long)m, k);
+    if (m > (int64_t)UINT32_MAX) return fail(c, KM_EINVAL, "a sample of %lld rows exceeds 32-bit row indices", (long long)m);
+    if (first < 0 || first >= m) return fail(c, KM_EINVAL, "first pick %lld is outside the sample", (long long)first);
+    if (km_pp_trials(k) > KM_PP_MAX_TRIALS) return fail(c, KM_EINVAL, "n_clusters=%d is too large for k-means++ seeding", k);
+    for (int64_t j = 0; j < m; j++)
+        if (sample[j] < 0 || sample[j] >= c->n || (j > 0 && sample[j] < sample[j - 1]))
+            return fail(c, KM_EINVAL, "sample rows must be ascending row indices below %lld", (long long)c->n);
+    HIPCHK(c, hipSetDevice(c->device));
+    const int d = c->d;
+    HIPCHK(c, c->pp_S.ensure((size_t)m * d));
+    HIPCHK(c, c->pp_C.ensure((size_t)k * d));
+    HIPCHK(c, c->pp_idx.ensure((size_t)m));
+    HIPCHK(c, c->pp_ws.ensure(km_pp_workspace(m, k)));
+    // the sample's rows, slice by slice (the indices are ascending, so each slice takes one contiguous range)
+    std::vector<int64_t> local(sample, sample + m);
+    std::vector<int64_t> j0s, j1s;
+    int64_t off = 0, j = 0;
+    for (auto &p : c->parts) {
+        const int64_t a = j;
+        while (j < m && sample[j] < off + p.rows) {
+            local[j] -= off;
+            j++;
+        }
+        j0s.push_back(a);
+        j1s.push_back(j);
+        off += p.rows;
+    }
+    HIPCHK(c, hipMemcpyAsync(c->pp_idx.p, local.data(), (size_t)m * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, launch(c, KK_SEED_PP, [&] {
+        for (size_t q = 0; q < c->parts.size(); q++) {
+            hipError_t e = km_launch_pp_gather(c->parts[q].X, c->pp_idx.p, j0s[q], j1s[q], m, d, c->pp_S.p, c->stream);
+            if (e != hipSuccess) return e;
+        }
+        return km_launch_pp(c->pp_S.p, m, d, k, first, seeds, c->pp_ws.p, c->pp_C.p, c->stream);
+    }));
+    HIPCHK(c, hipMemcpyAsync(C_out, c->pp_C.p, (size_t)k * d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
     harvest(c);
     return KM_OK;
 }

@@ -33,6 +33,8 @@ SIGNATURES = [
     ("km_lloyd_step", _c.c_int32, [_c.c_void_p, _f32p, _c.c_int32, _c.c_int32, _c.c_int32, _f32p, _f64p, _i32p]),
     ("km_fit", _c.c_int32, [_c.c_void_p, _f32p, _c.c_int32, _c.c_int32, _c.c_double, _c.c_int32, _c.c_int32,
                             _f32p, _f64p, _i32p, _i32p]),
+    ("km_seed_pp", _c.c_int32, [_c.c_void_p, _c.c_int32, _i64p, _c.c_int64, _c.c_int64,
+                                _c.POINTER(_c.c_uint64), _f32p]),
     ("km_profile", _c.c_int32, [_c.c_void_p, _c.c_int32]),
     ("km_profile_read", _c.c_int32, [_c.c_void_p, _c.c_int32, _f64p, _i64p]),
     ("km_kernel_name", _c.c_char_p, [_c.c_int32]),
@@ -150,6 +152,18 @@ class Context:
                                  1 if spherical else 0, _ptr(out, ctypes.c_float), ctypes.byref(inertia),
                                  ctypes.byref(n_iter), ctypes.byref(n_rel)))
         return out, inertia.value, n_iter.value, n_rel.value
+
+    def seed_pp(self, k, sample, first, seeds):
+        """-> (k, dims) float32: greedy k-means++ on the device over the sample rows (ascending global row
+        indices), starting from sample[first], with k - 1 per-round uint64 seeds."""
+        sample = np.ascontiguousarray(sample, dtype=np.int64)
+        seeds = np.ascontiguousarray(seeds, dtype=np.uint64)
+        if seeds.size == 0:
+            seeds = np.zeros(1, np.uint64)
+        out = np.empty((int(k), self.dims), np.float32)
+        self._check(lib().km_seed_pp(self._h, int(k), _ptr(sample, ctypes.c_int64), sample.shape[0], int(first),
+                                     _ptr(seeds, ctypes.c_uint64), _ptr(out, ctypes.c_float)))
+        return out
 
     # ---- timing and diagnostics
     def profile(self, enable=True):

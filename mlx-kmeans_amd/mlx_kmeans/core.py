@@ -6,7 +6,7 @@ install:
     lloyd_step(parts, C)                      core.py:2209-2242  -> (C_new f32, inertia, n_empty)
     assign_mlx(parts, C, return_labels=...)   core.py:2200-2206  -> (sums f64, counts i64, inertia[, labels i64])
     _gpu_pass(parts, C)                       core.py:2018-2197  -> (tot f64 (k, d+2), [(labels u32, best f32)])
-    kmeans_pp_init(parts, rows, k, rng)       core.py:153-192    greedy k-means++ on a subsample
+    kmeans_pp_init(parts, rows, k, rng)       core.py:153-192    greedy k-means++ on a subsample, on the GPU
     make_data_numpy, slice_rows, take_rows    core.py:19-40, 131-143
     kmeans(parts, rows, k, max_iter, tol, seed)   core.py:2247-2273
 
@@ -146,35 +146,27 @@ def take_rows(parts, idx):
 # ---------------------------------------------------------------- init
 
 def kmeans_pp_init(parts, rows, k, rng, sample=None):
-    """Greedy k-means++ (the algorithm of core.py:153-192, and scikit-learn's) on a random subsample.
+    """Greedy k-means++ on a random sample of the rows, every round on the GPU (core.py:153-192).
 
-    The sample is min(200k, max(20k, 20 k)) rows unless given, drawn without replacement and sorted. Round r draws
-    2 + floor(ln k) candidates with probability proportional to the current squared distance d2 and keeps the one
-    that lowers sum(d2) the most. Runs on the host in float64 on the sample only; the random stream is numpy's,
-    so the centres are not the reference's Metal-drawn ones.
+    The sample is min(200k, max(20k, 20 k)) rows unless given, drawn without replacement and sorted; then the
+    first pick and k - 1 per-round seeds are drawn from rng, in the reference's order, so one rng state gives one
+    seeding. Round r draws 2 + floor(ln k) candidates with probability proportional to each row's squared distance
+    to the nearest pick so far (a counter-based hash of the round's seed, the row and the trial; the reference's
+    Gumbel-max draw) and keeps the one that lowers the summed squared distance the most. -> (k, dims) float32.
     """
-    if sample is None:
-        sample = min(200_000, max(20_000, 20 * k))
-    idx = np.sort(rng.choice(rows, size=min(sample, rows), replace=False))
-    S = take_rows(parts, idx).astype(np.float64)
-    m = len(S)
-    trials = 2 + int(np.log(k)) if k > 1 else 1
-    ssq = (S * S).sum(1)
-    first = int(rng.integers(m))
-    picks = [first]
-    d2 = np.maximum(ssq + ssq[first] - 2.0 * (S @ S[first]), 0.0)
-    for _ in range(k - 1):
-        total = d2.sum()
-        if total > 0:
-            cand = rng.choice(m, size=trials, p=d2 / total)
-        else:
-            cand = rng.integers(m, size=trials)
-        dist = np.maximum(ssq[None, :] + ssq[cand][:, None] - 2.0 * (S[cand] @ S.T), 0.0)
-        mins = np.minimum(d2[None, :], dist)
-        b = int(np.argmin(mins.sum(1)))
-        d2 = mins[b]
-        picks.append(int(cand[b]))
-    return S[picks].astype(np.float32)
+    dd = parts if isinstance(parts, DeviceData) else DeviceData(_as_list(parts))
+    try:
+        if k > rows:
+            raise ValueError(f"n_samples={rows} should be >= n_clusters={k}.")
+        if sample is None:
+            sample = min(200_000, max(20_000, 20 * k))
+        idx = np.sort(rng.choice(rows, size=min(sample, rows), replace=False))
+        first = int(rng.integers(len(idx)))
+        seeds = rng.integers(2**63 - 1, size=k - 1).astype(np.uint64)
+        return dd.ctx.seed_pp(k, idx, first, seeds)
+    finally:
+        if dd is not parts:
+            dd.close()
 
 
 # ---------------------------------------------------------------- passes

@@ -16,7 +16,34 @@ Every generator takes n (rows) so tests can draw the same distribution at smalle
 """
 import numpy as np
 
-from .core import kmeans_pp_init
+from .core import take_rows
+
+
+def kmeans_pp_init(parts, rows, k, rng, sample=None):
+    """Start centres of the synthetic workloads: greedy k-means++ on the host in float64 (the algorithm of
+    core.py:153-192 with numpy's random stream), kept as it was so that each workload's start stays the same."""
+    if sample is None:
+        sample = min(200_000, max(20_000, 20 * k))
+    idx = np.sort(rng.choice(rows, size=min(sample, rows), replace=False))
+    S = take_rows(parts, idx).astype(np.float64)
+    m = len(S)
+    trials = 2 + int(np.log(k)) if k > 1 else 1
+    ssq = (S * S).sum(1)
+    first = int(rng.integers(m))
+    picks = [first]
+    d2 = np.maximum(ssq + ssq[first] - 2.0 * (S @ S[first]), 0.0)
+    for _ in range(k - 1):
+        total = d2.sum()
+        if total > 0:
+            cand = rng.choice(m, size=trials, p=d2 / total)
+        else:
+            cand = rng.integers(m, size=trials)
+        dist = np.maximum(ssq[None, :] + ssq[cand][:, None] - 2.0 * (S[cand] @ S.T), 0.0)
+        mins = np.minimum(d2[None, :], dist)
+        b = int(np.argmin(mins.sum(1)))
+        d2 = mins[b]
+        picks.append(int(cand[b]))
+    return S[picks].astype(np.float32)
 
 CHUNK = 4_000_000
 

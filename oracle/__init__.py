@@ -15,6 +15,9 @@ Two layers:
       reference_lloyd_step  tests/accuracy.py:108-129 float64 Lloyd step with the relocation rules
   * kmeans_simple_pass: numpy restatement of kmeans_simple.py:45-78 (the reference's teaching CPU path:
     expanded-form distances, argmin, scatter-add, float64 totals). It is NOT exact; it is only timed.
+  * seed_pp: numpy restatement of the reference's GPU k-means++ seeding (core.py:153-192 with its kernels
+    _PP_PICK_SRC / _PP_EVAL_SRC, 70-106, and the hash of 43-48): counter-based candidate draws, direct-form
+    float32 distances, float64 totals added in the device's order, so the device's picks must match bit for bit.
 """
 import ctypes
 import os
@@ -244,3 +247,83 @@ def kmeans_simple_pass(X, C, chunk=2_000_000):
         counts += cc
         err += ce
     return sums, counts, err
+
+
+# ---------------------------------------------------------------- k-means++ seeding
+
+def mix64(z):
+    """splitmix64's output function on uint64 arrays (the reference's mix64, mlx_kmeans/core.py:43-48)."""
+    z = np.asarray(z, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = z + np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def pp_trials(k):
+    """Candidates per round: 2 + floor(ln k) (core.py:181)."""
+    return 2 + int(np.log(k)) if k > 1 else 1
+
+
+def direct_sq(S, c):
+    """Float32 |S_i - c|^2 in the direct form, dims ascending, product and add rounded separately."""
+    s = np.zeros(len(S), np.float32)
+    for j in range(S.shape[1]):
+        q = S[:, j] - c[j]
+        s = s + q * q
+    return s
+
+
+def pp_keys(d2, seed, trials, t):
+    """Candidate keys of one trial: d2_i / (-ln u_i) in float64, u_i from the round's seed, the row and the trial
+    (the ordering of the reference's Gumbel-max key ln d2 - ln(-ln u), core.py:70-76)."""
+    i = np.arange(len(d2), dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        h = mix64(np.uint64(seed) ^ mix64(i * np.uint64(trials) + np.uint64(t)))
+    u = ((h >> np.uint64(40)).astype(np.float64) + 0.5) * 2.0**-24
+    return np.maximum(d2.astype(np.float64), 1e-30) / -np.log(u)
+
+
+def pp_block_total(v, block=32, lanes=64):
+    """Float64 sum of float32 values the way the seeding kernels add them: per block of 32 rows a halving tree
+    (element i += element i + h, h = 16 .. 1); then lane l of 64 adds the block sums b = l (mod 64) in ascending
+    order, and the 64 lane sums go through a halving tree (lane l += lane l + h, h = 32 .. 1)."""
+    v = v.astype(np.float64)
+    nb = (len(v) + block - 1) // block
+    x = np.zeros((nb, block))
+    x.reshape(-1)[:len(v)] = v
+    h = block // 2
+    while h:
+        x[:, :h] += x[:, h:2 * h]
+        h //= 2
+    bs = x[:, 0]
+    ls = np.zeros(lanes)
+    for b in range(nb):
+        ls[b % lanes] = ls[b % lanes] + bs[b]
+    h = lanes // 2
+    while h:
+        ls[:h] += ls[h:2 * h]
+        h //= 2
+    return float(ls[0])
+
+
+def seed_pp(S, k, first, seeds):
+    """Greedy k-means++ on the sample rows S (m, d) float32 -> (picked row indices, (k, d) float32 centres).
+
+    Restates the reference's GPU seeding (core.py:153-192 with _PP_PICK_SRC / _PP_EVAL_SRC, 70-106): d2 starts
+    as the direct-form distance to S[first]; round r draws, per trial t, the row with the largest key (lowest row
+    on a tie), scores min(d2, distance to that row) per row, and keeps the first trial with the smallest total;
+    its minima become d2."""
+    S = np.ascontiguousarray(S, dtype=np.float32)
+    trials = pp_trials(k)
+    d2 = direct_sq(S, S[first])
+    picks = [int(first)]
+    for r in range(k - 1):
+        cand = [int(np.argmax(pp_keys(d2, int(seeds[r]), trials, t))) for t in range(trials)]
+        mins = [np.fmin(d2, direct_sq(S, S[c])) for c in cand]
+        tot = [pp_block_total(m_) for m_ in mins]
+        b = int(np.argmin(tot))
+        d2 = mins[b]
+        picks.append(cand[b])
+    return np.array(picks), S[picks].copy()
