@@ -101,7 +101,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=50,
+                    help="untimed passes first: the GPU's clocks take some tens of milliseconds of work to settle")
     ap.add_argument("--workload", default="outliers_d32", choices=sorted(DESCRIPTIONS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--approx", action="store_true",
