@@ -55,6 +55,12 @@ __device__ __forceinline__ float lowd_vmin(float a, float b) {
     asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
+// v_min3_f32: two v_min_f32 in a row by definition (the same result for every input, NaN included)
+__device__ __forceinline__ float lowd_vmin3(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 
 // Largest k * (d + 2) served: the tiles take 256 bytes per entry.
 static constexpr int KM_LOWD_MAX_KW = 224;
@@ -211,7 +217,31 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
 #pragma unroll
                 for (int j = 0; j < D; j++) xs[i][j] = xr[i][j] - o[j];
             }
-            for (int c = 0; c < k; c++) {
+            // two centres at a time: the smallest of {m1, m2, a, b} is min3(m1, a, b) (m1 <= m2), the second the
+            // smaller of m2 and the middle of (m1, a, b)
+            int c = 0;
+            for (; c + 1 < k; c += 2) {
+                float q[D + 1], p[D + 1];
+#pragma unroll
+                for (int j = 0; j <= D; j++) {
+                    q[j] = Q[c * (D + 1) + j];
+                    p[j] = Q[(c + 1) * (D + 1) + j];
+                }
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    float a = q[D], b = p[D];
+#pragma unroll
+                    for (int j = 0; j < D; j++) {
+                        a = __builtin_fmaf(xs[i][j], q[j], a);
+                        b = __builtin_fmaf(xs[i][j], p[j], b);
+                    }
+                    const float ka = __uint_as_float((__float_as_uint(a) & ~imask) | (uint32_t)c);
+                    const float kb = __uint_as_float((__float_as_uint(b) & ~imask) | (uint32_t)(c + 1));
+                    m2[i] = lowd_vmin(m2[i], __builtin_amdgcn_fmed3f(m1[i], ka, kb));
+                    m1[i] = lowd_vmin3(m1[i], ka, kb);
+                }
+            }
+            if (c < k) {
                 float q[D + 1];
 #pragma unroll
                 for (int j = 0; j <= D; j++) q[j] = Q[c * (D + 1) + j];
