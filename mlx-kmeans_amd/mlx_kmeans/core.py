@@ -154,10 +154,10 @@ def kmeans_pp_init(parts, rows, k, rng, sample=None):
     to the nearest pick so far (a counter-based hash of the round's seed, the row and the trial; the reference's
     Gumbel-max draw) and keeps the one that lowers the summed squared distance the most. -> (k, dims) float32.
     """
+    if k > rows:
+        raise ValueError(f"n_samples={rows} should be >= n_clusters={k}.")
     dd = parts if isinstance(parts, DeviceData) else DeviceData(_as_list(parts))
     try:
-        if k > rows:
-            raise ValueError(f"n_samples={rows} should be >= n_clusters={k}.")
         if sample is None:
             sample = min(200_000, max(20_000, 20 * k))
         idx = np.sort(rng.choice(rows, size=min(sample, rows), replace=False))
