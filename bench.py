@@ -101,8 +101,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=50,
-                    help="untimed passes first: the GPU's clocks take some tens of milliseconds of work to settle")
+    ap.add_argument("--warmup", type=int, default=0,
+                    help="untimed passes first; 0 (default): as many as fill 0.3 s, at least 3 (the GPU's clocks "
+                         "take some tens of milliseconds of work to settle)")
     ap.add_argument("--workload", default="outliers_d32", choices=sorted(DESCRIPTIONS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--approx", action="store_true",
@@ -143,7 +144,15 @@ def main():
     # warmup, then exactly `steps` Lloyd iterations timed by the host clock around device synchronisations.
     # tol = -1 never stops the loop, so a workload that reaches a fixed point early still runs every pass.
     mode = _lib.KM_APPROX if a.approx else _lib.KM_EXACT
-    ctx.fit(C0, a.warmup, -1.0, mode=mode)
+    if a.warmup > 0:
+        ctx.fit(C0, a.warmup, -1.0, mode=mode)
+        warm = a.warmup
+    else:
+        warm, tw = 0, time.perf_counter()
+        while warm < 3 or time.perf_counter() - tw < 0.3:
+            ctx.fit(C0, 10, -1.0, mode=mode)
+            torch.cuda.synchronize()
+            warm += 10
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     C, inertia, iters, _ = ctx.fit(C0, a.steps, -1.0, mode=mode)
@@ -180,7 +189,7 @@ def main():
         "unit": "ms/pass",
         "n_gpus": 1,
         "steps": a.steps,
-        "warmup": a.warmup,
+        "warmup": warm,
         "ms_per_step": round(ms, 5),
         "higher_is_better": False,
         "scaling": "weak",
