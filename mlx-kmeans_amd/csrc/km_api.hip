@@ -326,7 +326,7 @@ static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
     if (path == KM_PATH_ROWS) return FAM_ROWS;
     if (path == KM_PATH_MFMA) return mp->ok ? FAM_MFMA_FUSED : wide_ok ? FAM_BIG : -1;
     if (path == KM_PATH_FUSED) return lowd_ok ? FAM_LOWD : -1;
-    if (mp->ok && c->d >= 16 && (int64_t)k * c->d >= 256) return FAM_MFMA_FUSED;
+    if (mp->ok && c->d >= 16 && (int64_t)k * c->d >= 192) return FAM_MFMA_FUSED;
     if (lowd_ok) return FAM_LOWD;
     if (wide_ok && (int64_t)k * c->d >= 1024) return FAM_BIG;
     return FAM_ROWS;

@@ -122,6 +122,7 @@ struct km_lowd_plan {
     int64_t rbs;     // rows per block
     int nrb;         // blocks
     size_t lds;      // dynamic LDS bytes
+    int lsh;         // the wave keeps 64 >> lsh tile columns; 1 << lsh lanes take turns on each
 };
 km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned);
 hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int d, const float *C, int k,

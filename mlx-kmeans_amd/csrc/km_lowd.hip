@@ -17,14 +17,17 @@
 // only if a_c - a_m <= 2E + 2 g/(1-g) D_m, with D_m <= |x|^2 + a_m + E; the packed index perturbs a key by at
 // most RHO relative, which the test absorbs.
 //
-// Accumulation, deterministic by construction. A block is one wave. Every lane has a private float32 tile
-// [count, best, x_0 .. x_{D-1}] x k clusters in LDS, laid out [cluster][column][lane]: a lane adds its row
-// into its own column of addresses (one LDS bank per lane, so no conflicts and no shared address), in row
-// order. Every FOLD_ROWS rows per lane the wave folds the 64 tiles into float64 accumulators - each entry summed
-// over the lanes in a fixed rotation - and clears them, so no float32 accumulator ever adds more than
-// FOLD_ROWS values (the reference adds 1024-row partials in plain float32 too, core.py:1562-1636). At the end
-// the wave writes its float64 accumulators as one (sum, compensation) float32 pair per entry: the per-block
-// partial that the fixed-order reduction reads.
+// Accumulation, deterministic by construction. A block is one wave. The wave keeps L = 64 >> lsh float32 tiles
+// [count, best, x_0 .. x_{D-1}] x k clusters in LDS, laid out [cluster][column][L]: lane l adds its rows into
+// column l % L, and the 64 / L lanes that share a column take turns in lane order (one pass per lane group, so
+// each tile address has one writer per pass and the LDS executes the passes in program order). The L lanes of
+// a pass touch L distinct consecutive columns: no bank conflicts. Every FOLD_ROWS additions per column the wave
+// folds the tiles into float64 accumulators - each entry summed over the columns in a fixed rotation - and
+// clears them, so no float32 accumulator ever adds more than FOLD_ROWS values (the reference adds 1024-row
+// partials in plain float32 too, core.py:1562-1636). At the end the wave writes its float64 accumulators as one
+// (sum, compensation) float32 pair per entry: the per-block partial that the fixed-order reduction reads. The
+// plan picks the largest L whose LDS footprint still lets the register-limited number of waves reside: shared
+// columns cost one LDS pass per lane group, private ones cost occupancy once k (d + 2) grows.
 #pragma clang fp contract(off)
 #include "km_internal.h"
 #include <math.h>
@@ -32,18 +35,20 @@
 template <int D>
 struct LowGeo {
     static constexpr int W = D + 2;                                // columns: count, best, dims
-    static constexpr int R = D <= 4 ? 8 : D <= 8 ? 4 : 2;          // rows per lane per iteration
-    static constexpr int FOLD_ROWS = 256;                          // rows per lane between float64 folds
-    static constexpr int FOLD_IT = FOLD_ROWS / R;                  // iterations between folds
+    // rows per lane per iteration: the loads in flight while the previous rows are scored
+    static constexpr int R = D <= 8 ? 8 : 4;
+    static constexpr int FOLD_ROWS = 256;                          // additions per tile column between folds
+    static constexpr int FOLD_IT = FOLD_ROWS / R;                  // iterations between folds with private columns
 };
 
 __host__ __device__ constexpr size_t km_al16(size_t v) { return (v + 15) / 16 * 16; }
 
-// LDS bytes of one block (one wave): centres, the 64 lane tiles, the float64 accumulators, and with the screen
-// the centres as [-2c, |c|^2] rows
-__host__ __device__ inline size_t km_lowd_lds(int d, int k, bool screen) {
+// LDS bytes of one block (one wave): centres, the 64 >> lsh tiles, the float64 accumulators, and with the
+// screen the centres as [-2c, |c|^2] rows
+__host__ __device__ inline size_t km_lowd_lds(int d, int k, bool screen, int lsh) {
     const size_t kw = (size_t)k * (d + 2);
-    return km_al16((size_t)k * d * 4) + kw * 64 * 4 + kw * 8 + (screen ? km_al16((size_t)k * (d + 1) * 4) : 0);
+    return km_al16((size_t)k * d * 4) + kw * (64 >> lsh) * 4 + kw * 8 +
+           (screen ? km_al16((size_t)k * (d + 1) * 4) : 0);
 }
 
 __host__ __device__ constexpr double km_lowd_gamma(int m) {
@@ -62,8 +67,18 @@ __device__ __forceinline__ float lowd_vmin3(float a, float b, float c) {
     return r;
 }
 
-// Largest k * (d + 2) served: the tiles take 256 bytes per entry.
-static constexpr int KM_LOWD_MAX_KW = 224;
+// Largest k * (d + 2) served: the shared tiles (64 bytes per entry), the float64 accumulators (8) and the centres
+// (under 8) stay within 64 KB of LDS.
+static constexpr int KM_LOWD_MAX_KW = 768;
+// Shared tile columns: 4 lanes take turns on each of 16 columns (the fold interval (256 / R) >> 2 stays at
+// least one iteration for every R <= 16).
+static constexpr int KM_LOWD_SHARED_LSH = 2;
+// Shared columns cost four LDS read-modify-write passes per iteration instead of one; they pay only when the
+// private layout leaves few waves per CU or few row bytes in flight per CU (measured on MI355X, 20M rows: d = 8,
+// k = 12: 531 -> 214 us with 4 private waves; d = 4, k = 16: 171 -> 137 us with 6; d = 2, k = 16: 102 -> 86 us
+// with 9 waves holding 36 KB; but d = 8, k = 8 with 7 waves holding 112 KB: private 154 us, shared 173 us).
+static constexpr int KM_LOWD_PRIVATE_MIN_WAVES = 6;
+static constexpr int64_t KM_LOWD_PRIVATE_MIN_BYTES = 48 * 1024;
 
 template <int D>
 __device__ __forceinline__ void load_row(const float *__restrict__ X, int64_t row, float (&x)[D]) {
@@ -97,23 +112,23 @@ __device__ __forceinline__ void wave_sync_lds() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// F[e] += sum over lanes of T[e][lane], lanes taken in the fixed rotation lane, lane+1, ... (mod 64) so the 64
-// lanes read 64 distinct banks; then the tiles are cleared.
-__device__ __forceinline__ void fold_tiles(float *T, double *F, int kw, int lane) {
+// F[e] += sum over the L columns of T[e], taken in the fixed rotation lane, lane+1, ... (mod L) so that lanes
+// spread over the banks; then the tiles are cleared.
+__device__ __forceinline__ void fold_tiles(float *T, double *F, int kw, int L, int lane) {
     wave_sync_lds();
     for (int e = lane; e < kw; e += 64) {
-        const float *row = T + (size_t)e * 64;
+        const float *row = T + (size_t)e * L;
         double s = 0.0;
 #pragma unroll 8
-        for (int l = 0; l < 64; l++) s += (double)row[(l + lane) & 63];
+        for (int l = 0; l < L; l++) s += (double)row[(l + lane) & (L - 1)];
         F[e] += s;
     }
     wave_sync_lds();
-    for (int e = lane; e < kw * 64; e += 64) T[e] = 0.0f;
+    for (int e = lane; e < kw * L; e += 64) T[e] = 0.0f;
     wave_sync_lds();
 }
 
-template <int D, bool SCR>
+template <int D, bool SCR, int LSH>
 __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, int64_t n,
                                                    const float *__restrict__ C, int k, int64_t rbs,
                                                    uint32_t *__restrict__ labels, float *__restrict__ best,
@@ -136,13 +151,15 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
     extern __shared__ float lds[];
     const int lane = threadIdx.x;
     const int kw = k * W;
+    constexpr int L = 64 >> LSH;                                          // tile columns
+    constexpr int fold_it = G::FOLD_IT >> LSH;                            // 64 / L lanes add to each column
     float *Cl = lds;
-    float *T = lds + km_al16((size_t)k * D * 4) / 4;                      // [kw][64]
-    double *F = reinterpret_cast<double *>(T + (size_t)kw * 64);          // [kw]
+    float *T = lds + km_al16((size_t)k * D * 4) / 4;                      // [kw][L]
+    double *F = reinterpret_cast<double *>(T + (size_t)kw * L);           // [kw]
     float *Q = reinterpret_cast<float *>(F + kw);                         // [k][D + 1]: -2c, |c|^2 (screen)
 
     for (int e = lane; e < k * D; e += 64) Cl[e] = C[e];
-    for (int e = lane; e < kw * 64; e += 64) T[e] = 0.0f;
+    for (int e = lane; e < kw * L; e += 64) T[e] = 0.0f;
     for (int e = lane; e < kw; e += 64) F[e] = 0.0;
     // screen constants: the shift o, max |c'| (rounded up), max |c'|^2, and the index bits packed into keys
     float cnmax = 0.0f, csqmax = 0.0f;
@@ -352,23 +369,35 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                 }
             }
         }
-        // outputs, then each row into this lane's tile
+        // outputs, then each row into this lane's tile column, one lane group after another
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const int64_t row = r0 + 64 * i + lane;
             if (row < r_end) {
                 if (labels) labels[row] = bl[i];
                 if (best) best[row] = bst[i];
-                float *t = T + (size_t)bl[i] * (W * 64) + lane;
-                t[0] += 1.0f;
-                t[64] += bst[i];
-#pragma unroll
-                for (int j = 0; j < D; j++) t[(2 + j) * 64] += xr[i][j];
             }
         }
-        if (++it == G::FOLD_IT) {
+        const int grp = lane / L;
+#pragma unroll
+        for (int g = 0; g < (1 << LSH); g++) {
+            if (LSH == 0 || grp == g) {
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    const int64_t row = r0 + 64 * i + lane;
+                    if (row < r_end) {
+                        float *t = T + (size_t)bl[i] * (W * L) + (lane % L);
+                        t[0] += 1.0f;
+                        t[L] += bst[i];
+#pragma unroll
+                        for (int j = 0; j < D; j++) t[(2 + j) * L] += xr[i][j];
+                    }
+                }
+            }
+        }
+        if (++it == fold_it) {
             it = 0;
-            fold_tiles(T, F, kw, lane);
+            fold_tiles(T, F, kw, L, lane);
         }
         if (more) {
 #pragma unroll
@@ -377,7 +406,7 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                 for (int j = 0; j < D; j++) xr[i][j] = xn[i][j];
         }
     }
-    if (it) fold_tiles(T, F, kw, lane);
+    if (it) fold_tiles(T, F, kw, L, lane);
     // this block's partial as a float32 (sum, compensation) pair per entry
     float *ps = psum + (int64_t)(rb0 + blockIdx.x) * kw;
     float *pc = pcomp + (int64_t)(rb0 + blockIdx.x) * kw;
@@ -394,17 +423,20 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
 typedef void (*lowd_fn)(const float *, int64_t, const float *, int, int64_t, uint32_t *, float *, float *, float *,
                         int, const int32_t *);
 
-#define KM_LOWD_FNS(S)                                                                                        \
-    {nullptr,              k_fused_lowd<1, S>,  k_fused_lowd<2, S>,  k_fused_lowd<3, S>,  k_fused_lowd<4, S>,  \
-     k_fused_lowd<5, S>,  k_fused_lowd<6, S>,  k_fused_lowd<7, S>,  k_fused_lowd<8, S>,  k_fused_lowd<9, S>,   \
-     k_fused_lowd<10, S>, k_fused_lowd<11, S>, k_fused_lowd<12, S>, k_fused_lowd<13, S>, k_fused_lowd<14, S>,  \
-     k_fused_lowd<15, S>, k_fused_lowd<16, S>}
-static lowd_fn g_lowd[2][17] = {KM_LOWD_FNS(false), KM_LOWD_FNS(true)};
+#define KM_LOWD_FNS(S, H)                                                                                     \
+    {nullptr,                k_fused_lowd<1, S, H>,  k_fused_lowd<2, S, H>,  k_fused_lowd<3, S, H>,              \
+     k_fused_lowd<4, S, H>,  k_fused_lowd<5, S, H>,  k_fused_lowd<6, S, H>,  k_fused_lowd<7, S, H>,              \
+     k_fused_lowd<8, S, H>,  k_fused_lowd<9, S, H>,  k_fused_lowd<10, S, H>, k_fused_lowd<11, S, H>,             \
+     k_fused_lowd<12, S, H>, k_fused_lowd<13, S, H>, k_fused_lowd<14, S, H>, k_fused_lowd<15, S, H>,             \
+     k_fused_lowd<16, S, H>}
+// [screen][shared columns][dims]
+static lowd_fn g_lowd[2][2][17] = {{KM_LOWD_FNS(false, 0), KM_LOWD_FNS(false, KM_LOWD_SHARED_LSH)},
+                                   {KM_LOWD_FNS(true, 0), KM_LOWD_FNS(true, KM_LOWD_SHARED_LSH)}};
 #undef KM_LOWD_FNS
 
 static int g_lowd_cus = 0;
 
-static int lowd_rows_per_iter(int d) { return 64 * (d <= 4 ? 8 : d <= 8 ? 4 : 2); }
+static int lowd_rows_per_iter(int d) { return 64 * (d <= 8 ? 8 : 4); }
 
 // The screen costs d + 3 operations per centre and row against the direct form's 3d + 3, plus a per-row window
 // and one direct form with an LDS gather; measured on MI355X it is the faster of the two from about 24 centres on
@@ -417,7 +449,6 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
     if ((int64_t)k * (d + 2) > KM_LOWD_MAX_KW) return pl;
     if ((d % 2 == 0) && !aligned) return pl;   // vector row loads need 8/16-byte aligned rows
     const bool scr = lowd_screen(k);
-    const size_t lds = km_lowd_lds(d, k, scr);
     if (g_lowd_cus == 0) {
         int dev = 0;
         hipDeviceProp_t prop;
@@ -425,11 +456,22 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
             g_lowd_cus = prop.multiProcessorCount;
         if (g_lowd_cus <= 0) g_lowd_cus = 256;
     }
-    if (lds > 65536) return pl;
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)g_lowd[scr][d], 64, lds) != hipSuccess ||
-        occ < 1)
-        occ = 1;
+    // private tile columns unless sharing them lets more waves reside (LDS- rather than register-bound)
+    int occs[2] = {0, 0};
+    for (int h = 0; h < 2; h++) {
+        const size_t b = km_lowd_lds(d, k, scr, h ? KM_LOWD_SHARED_LSH : 0);
+        if (b > 65536 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&occs[h], (const void *)g_lowd[scr][h][d], 64,
+                                                                      b) != hipSuccess)
+            occs[h] = 0;
+    }
+    const int shared = occs[1] > occs[0] && (occs[0] <= KM_LOWD_PRIVATE_MIN_WAVES ||
+                                             (int64_t)occs[0] * lowd_rows_per_iter(d) * d * 4 < KM_LOWD_PRIVATE_MIN_BYTES)
+                           ? 1
+                           : 0;
+    const int occ = occs[shared];
+    if (occ < 1) return pl;
+    const int lsh = shared ? KM_LOWD_SHARED_LSH : 0;
+    const size_t lds = km_lowd_lds(d, k, scr, lsh);
     const int64_t unit = lowd_rows_per_iter(d);
     const int64_t units = (n + unit - 1) / unit;
     int64_t nrb = (int64_t)g_lowd_cus * occ;
@@ -442,6 +484,7 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
     pl.rbs = rbs;
     pl.nrb = (int)((n + rbs - 1) / rbs);
     pl.lds = lds;
+    pl.lsh = lsh;
     return pl;
 }
 
@@ -449,7 +492,7 @@ hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s) {
     if (!pl.ok || d < 1 || d > 16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(g_lowd[pl.screen ? 1 : 0][d], dim3(pl.nrb), dim3(64), pl.lds, s, X, n, C, k, pl.rbs, labels,
-                       best, psum, pcomp, rb0, stop);
+    hipLaunchKernelGGL(g_lowd[pl.screen ? 1 : 0][pl.lsh ? 1 : 0][d], dim3(pl.nrb), dim3(64), pl.lds, s, X, n, C, k,
+                       pl.rbs, labels, best, psum, pcomp, rb0, stop);
     return hipGetLastError();
 }

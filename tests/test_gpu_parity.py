@@ -39,8 +39,8 @@ def mfma_served(d, k):
 
 
 def fused_served(d, k):
-    """The fused single-read path serves dims <= 16 with k * (dims + 2) <= 224 (its per-lane LDS tiles)."""
-    return d <= 16 and k * (d + 2) <= 224
+    """The fused single-read path serves dims <= 16 with k * (dims + 2) <= 768 (its LDS tiles)."""
+    return d <= 16 and k * (d + 2) <= 768
 
 
 SERVED = {"rows": lambda d, k: True, "mfma": mfma_served, "fused": fused_served}
@@ -161,7 +161,7 @@ def test_paths_are_bit_identical(lib, d, k):
     ctx.close()
 
 
-@pytest.mark.parametrize("d,k", [(4, 32), (1, 70), (32, 64), (16, 32), (48, 100)])
+@pytest.mark.parametrize("d,k", [(4, 32), (1, 70), (32, 64), (16, 32), (48, 100), (8, 76), (2, 150)])
 def test_screen_edge_cases_match_the_rows_loop(lib, d, k):
     """The screened paths against the rows loop and the oracle on the cases a screen can get wrong: duplicate
     centres (exact ties, lowest index wins), rows equal to a centre (distance 0), NaN and infinite rows (label 0,
@@ -197,6 +197,34 @@ def test_screen_edge_cases_match_the_rows_loop(lib, d, k):
         assert np.array_equal(l1, l2), (name, np.flatnonzero(l1 != l2)[:10])
         assert np.array_equal(b1.view(np.uint32), b2.view(np.uint32)), name
     assert served
+    ctx.close()
+
+
+@pytest.mark.parametrize("d,k", [(3, 5), (2, 16), (4, 16), (16, 8), (2, 190), (8, 64), (12, 40), (16, 42)])
+def test_fused_tile_layouts_match_oracle(lib, d, k):
+    """The fused low-d path on both tile layouts (private columns at small k (d + 2), columns shared by four lanes
+    where the private ones would cap occupancy) up to its largest k (d + 2) = 768, over two uneven slices:
+    labels and best bit-identical to the oracle, counts exact, sums and inertia within tolerance, and a rerun
+    bit-identical."""
+    import oracle
+    rng = np.random.default_rng(300 + 7 * d + k)
+    n = 60_000
+    cen = rng.uniform(-3, 3, size=(k, d)).astype(np.float32)
+    X = (cen[rng.integers(0, k, n)] + 0.8 * rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(n, k, replace=False)].copy()
+    parts = [X[:20_011], X[20_011:]]
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    say(f"[gpu] fused tile layouts d={d} k={k}")
+    tot, labels, best = ctx.run_pass(C, path=lib.KM_PATH_FUSED, labels=True, best=True)
+    assert ctx.last_path() == "fused"
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(labels, ol), np.flatnonzero(labels != ol)[:10]
+    assert np.array_equal(best.view(np.uint32), ob.view(np.uint32))
+    check_totals(tot, X, labels, best, oracle.totals(X, ol, ob, k), scale)
+    t2, l2, b2 = ctx.run_pass(C, path=lib.KM_PATH_FUSED, labels=True, best=True)
+    assert np.array_equal(t2.view(np.uint64), tot.view(np.uint64))
     ctx.close()
 
 
