@@ -91,8 +91,9 @@ def _validate_parts(parts):
         raise ValueError(f"slices have {bad[0]} and {d} columns; every slice needs the same features")
 
 
-def _context(parts, C):
-    """-> (DeviceData, owned) for parts, checking the centres against them (core.py:2022-2035 wording)."""
+def _context(parts, C, method="auto"):
+    """-> (DeviceData, owned, kernel path) for parts, checking the centres against them (core.py:2022-2035
+    wording) and the method, all before any device work."""
     dd = parts if isinstance(parts, DeviceData) else None
     if dd is None:
         parts = _as_list(parts)
@@ -104,9 +105,10 @@ def _context(parts, C):
     if C.shape[1] != d:
         raise ValueError(f"data has {d} columns but the centers have {C.shape[1]}; "
                          f"fit and predict need the same features")
+    path = _path(method, C.shape[0], d)
     if dd is not None:
-        return dd, False
-    return DeviceData(parts), True
+        return dd, False, path
+    return DeviceData(parts), True, path
 
 
 def _path(method, k, d):
@@ -176,11 +178,10 @@ def _gpu_pass(parts, C, method="auto", accumulate="auto", iterate=False):
     per slice). core.py:2018-2197. `accumulate` is accepted for compatibility: every accumulation here is
     deterministic and compensated. `iterate` is accepted and has no effect (no per-dataset state is kept)."""
     del accumulate, iterate
-    dd, owned = _context(parts, C)
+    dd, owned, path = _context(parts, C, method)
     try:
         C = np.ascontiguousarray(C, dtype=np.float32)
-        tot, labels, best = dd.ctx.run_pass(C, _mode(method), _path(method, C.shape[0], dd.dims),
-                                            labels=True, best=True)
+        tot, labels, best = dd.ctx.run_pass(C, _mode(method), path, labels=True, best=True)
         out, a = [], 0
         rows_per = [p.shape[0] for p in (dd.parts if isinstance(dd.parts, list) else [dd.parts])]
         for r in rows_per:
@@ -196,11 +197,10 @@ def assign_mlx(parts, C, method="auto", return_labels=False, accumulate="auto"):
     """One Lloyd pass on the GPU -> (per-cluster sums f64 (k, d), counts i64 (k,), inertia[, labels i64 (n,)]).
     core.py:2200-2206."""
     del accumulate
-    dd, owned = _context(parts, C)
+    dd, owned, path = _context(parts, C, method)
     try:
         C = np.ascontiguousarray(C, dtype=np.float32)
-        tot, labels, _ = dd.ctx.run_pass(C, _mode(method), _path(method, C.shape[0], dd.dims),
-                                         labels=return_labels, best=False)
+        tot, labels, _ = dd.ctx.run_pass(C, _mode(method), path, labels=return_labels, best=False)
         result = (tot[:, 2:], np.rint(tot[:, 0]).astype(np.int64), float(tot[:, 1].sum()))
         if return_labels:
             result += (labels.astype(np.int64),)
@@ -217,10 +217,10 @@ def lloyd_step(parts, C, method="auto", accumulate="auto"):
     empty cluster, ties to the lower row index), which leave their old clusters; a cluster still empty takes the
     largest cluster's centre."""
     del accumulate
-    dd, owned = _context(parts, C)
+    dd, owned, path = _context(parts, C, method)
     try:
         C = np.ascontiguousarray(C, dtype=np.float32)
-        return dd.ctx.lloyd_step(C, _mode(method), _path(method, C.shape[0], dd.dims))
+        return dd.ctx.lloyd_step(C, _mode(method), path)
     finally:
         if owned:
             dd.close()
@@ -229,7 +229,7 @@ def lloyd_step(parts, C, method="auto", accumulate="auto"):
 def lloyd_fit(parts, C0, max_iter, tol=0.0, method="auto", spherical=False):
     """Up to max_iter Lloyd iterations from C0 with the stopping rule |prev - inertia| <= tol * prev, run back to
     back on the GPU (the loop of estimator.py:136-150) -> (C, last inertia, iterations, empties relocated)."""
-    dd, owned = _context(parts, C0)
+    dd, owned, _ = _context(parts, C0, method)
     try:
         return dd.ctx.fit(np.ascontiguousarray(C0, dtype=np.float32), max_iter, tol, _mode(method), spherical)
     finally:

@@ -66,3 +66,36 @@ def test_synthetic_workloads_small():
     # the start centres are rows of the data
     rows = {r.tobytes() for r in w["X"]}
     assert all(c.tobytes() in rows for c in w["C0"])
+
+
+def test_input_checks_raise_before_the_device(monkeypatch):
+    """The reference's reuse checks (tests/reuse.py:106-123) that need no GPU: a predict with another feature
+    count and method='tiles' with k % 8 != 0 raise ValueError before any device work, and input over the
+    per-slice element limit is cut into slices."""
+    from mlx_kmeans import KMeans, core
+    rng = np.random.default_rng(0)
+    m = KMeans.from_centers(rng.standard_normal((8, 8)).astype(np.float32))
+    with pytest.raises(ValueError, match="features"):
+        m.predict(rng.standard_normal((300, 16)).astype(np.float32))
+    X = rng.standard_normal((3000, 12)).astype(np.float32)
+    with pytest.raises(ValueError, match="tiles"):
+        core.assign_mlx([X], np.zeros((100, 12), np.float32), method="tiles")
+    monkeypatch.setattr(core, "PART_MAX_ELEMENTS", 1_000_000)
+    parts = KMeans._parts(np.zeros((2500, 1000), np.float32))
+    assert len(parts) == 3 and sum(len(p) for p in parts) == 2500
+
+
+def test_model_npz_format_loads_without_pickle(tmp_path):
+    """The reference's file workflow saves model.npz as centers, mean, scale, columns (files.py:178-179); it loads
+    with allow_pickle=False and its centres make a model through from_centers."""
+    from mlx_kmeans import KMeans
+    rng = np.random.default_rng(1)
+    C = rng.standard_normal((5, 3)).astype(np.float32)
+    np.savez(tmp_path / "model.npz", centers=C, mean=np.array([1.0, 2.0, 3.0]), scale=np.array([2.0, 1.0, 0.5]),
+             columns=np.array(["spend", "visits", "age"]))
+    z = np.load(tmp_path / "model.npz", allow_pickle=False)
+    assert list(z["columns"]) == ["spend", "visits", "age"]
+    m = KMeans.from_centers(z["centers"])
+    assert m.n_clusters == 5 and np.array_equal(m.cluster_centers_, C)
+    with pytest.raises(ValueError, match="NaN or infinity"):
+        KMeans.from_centers(np.full((2, 3), np.nan, np.float32))
