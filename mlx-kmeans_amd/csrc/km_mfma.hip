@@ -36,13 +36,17 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // ------------------------------------------------------------------ the fused kernel
 //
 // Exactness of the screen. For a row x and centre c let A_c = |c|^2 - 2 x.c (exact reals) and D_c = |x - c|^2 =
-// |x|^2 + A_c. The matrix cores give a'_c = sum_j bf16(x_j) (h_j + l_j) + q_h + q_l, where h_j + l_j is -2 c_j split
-// into two bf16 pieces (h = bf16(-2c_j), l = bf16(-2c_j - h): relative residual 2^-16) and q_h + q_l is |c|^2 the
-// same way. bf16 rounding to nearest has unit roundoff u = 2^-8 (1 + 2^-8 rounds to 1), so bf16(x_j) = x_j (1 + d),
-// |d| <= 2^-8; products of bf16 values are exact in float32 and the float32 accumulation of NACC = 2 DP + 2 terms
-// adds at most gamma_NACC times their absolute sum. With bf16 denormal flushing covered by FLUSH,
+// |x|^2 + A_c. The matrix cores give a'_c = sum_j bf16(x_j) h_j + q_h + q_l, where h_j = bf16(-2 c_j) and
+// q_h + q_l is |c|^2 split into two bf16 pieces (q_h = bf16(|c|^2), q_l = bf16(|c|^2 - q_h): relative residual
+// 2^-16). bf16 rounding to nearest has unit roundoff u = 2^-8 (1 + 2^-8 rounds to 1), so bf16(x_j) = x_j (1 + d) and
+// h_j = -2 c_j (1 + e) with |d|, |e| <= 2^-8: each product is -2 x_j c_j (1 + d + e + d e), within
+// 2 |x_j| |c_j| (2^-8 + 2^-8 + 2^-16) of the exact one, and sum_j |x_j| |c_j| <= |x| |c|. Products of bf16 values
+// are exact in float32 and the float32 accumulation of NACC = DP + 2 terms adds at most gamma_NACC times their
+// absolute sum. With bf16 denormal flushing covered by FLUSH,
 //     |a'_c - A_c| <= E = BETA |x| max|c| + GAM2 max|c|^2 + FLUSH (|x| + max|c|) + TINY      (uniform in c),
-//     BETA = 2 (2^-8 + 2^-16 + 2^-24) + 2.04 gamma_NACC,   GAM2 = 1.01 gamma_NACC + 2^-16 + 2^-23.
+//     BETA = 2 (2^-8 + 2^-8 + 2^-16) + 2.04 gamma_NACC,   GAM2 = 1.01 gamma_NACC + 2^-16 + 2^-23.
+// (A second bf16 piece of -2c, the residual, would shrink BETA's second 2^-8 to 2^-16 for one more MFMA per
+// K-step; the window it narrows is already wide of almost every row's runner-up, and the MFMAs are not free.)
 // The float32 direct form s_c of the rows loop satisfies |s_c - D_c| <= g D_c + eta, g = gamma_{D+2}. A centre c
 // can hold the row's minimum only if s_c <= s_m for the screen's minimiser m, which forces
 //     a'_c - a'_m <= 2E + 2 g/(1-g) D_m + tiny,   D_m <= |x|^2 + a'_m + E,
@@ -100,7 +104,7 @@ struct Geo {
     static constexpr int DP = (D + 15) / 16 * 16;   // padded dims
     static constexpr int DH = DP / 2;               // dims per lane half
     static constexpr int DS = DP / 16;              // MFMA K-steps over the dims
-    static constexpr int AK = 2 * DS + 1;           // A-operand K-steps: high pieces, low pieces, |c|^2
+    static constexpr int AK = DS + 1;               // A-operand K-steps: bf16(-2c), then |c|^2
     static constexpr int KT = KP / 32;              // centre tiles
     static constexpr int IB = KT <= 1 ? 4 : KT <= 2 ? 5 : 6;   // index bits packed into keys (16 KT values)
     static constexpr int CS = D + 1;                // LDS row stride of the float32 centres (odd: lanes reading
@@ -138,10 +142,7 @@ __device__ __forceinline__ void screen_tile(const bf16x8 (&B)[Geo<D, KP>::DS], c
         a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][0], B[0], zero, 0, 0, 0);
 #pragma unroll
         for (int s = 1; s < G::DS; s++) a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][s], B[s], a[t], 0, 0, 0);
-#pragma unroll
-        for (int s = 0; s < G::DS; s++)
-            a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][G::DS + s], B[s], a[t], 0, 0, 0);
-        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][2 * G::DS], Bone, a[t], 0, 0, 0);
+        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Aop[t][G::DS], Bone, a[t], 0, 0, 0);
     }
 }
 
@@ -166,18 +167,19 @@ __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], flo
 
 // Candidate bits of this lane's screen values: bit (8(v/4) + 4h + v%4) of word t is set when a[t][v] <= T2. The
 // values are compared unpacked; T2 = T + 4 RHO |T| + tiny covers the packing perturbation, so the set contains
-// every centre the packed-key test would admit. Two instructions per value: v_cmp into vcc, then v_addc shifts
-// the bit in (m = 2m + vcc), v = 15 first so bit v lands at position v; a nibble-to-byte spread places them.
+// every centre the packed-key test would admit. The bits shift in with v = 15 first, so bit v lands at position v;
+// a nibble-to-byte spread places them.
 template <int D, int KP>
 __device__ __forceinline__ void cand_bits(const f32x16 (&a)[Geo<D, KP>::KT], float T2, int h,
                                           uint32_t (&w)[Geo<D, KP>::KT]) {
     using G = Geo<D, KP>;
 #pragma unroll
     for (int t = 0; t < G::KT; t++) {
+        // compiled code, not inline asm: the values are matrix-core results, and only the compiler's hazard
+        // tracking inserts the wait states a vector instruction needs before it may read them
         uint32_t m = 0;
 #pragma unroll
-        for (int v = 15; v >= 0; v--)
-            asm("v_cmp_ge_f32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc" : "+v"(m) : "v"(T2), "v"(a[t][v]) : "vcc");
+        for (int v = 15; v >= 0; v--) m = 2u * m + (a[t][v] <= T2 ? 1u : 0u);
         // byte j = nibble j of the 16-bit mask
         const uint32_t p = __builtin_amdgcn_perm(m, m, 0x01010000u);   // bytes b0, b0, b1, b1
         const uint32_t q = ((p & 0x000f000fu) | ((p >> 4) & 0x0f000f00u));
@@ -349,8 +351,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     constexpr bool OHB = NT == 1 && OHB_BYTES <= L::BUF;
     constexpr int WBYTES = (LOOPB > FOLD + 4 * KP) ? LOOPB : FOLD + 4 * KP;
     // window constants
-    constexpr int NACC = 2 * G::DP + 2;
-    constexpr float BETA = (float)((2.0 * (0x1p-8 + 0x1p-16 + 0x1p-24) + 2.04 * km_gamma(NACC)) * (1.0 + 0x1p-20));
+    constexpr int NACC = G::DP + 2;
+    constexpr float BETA = (float)((2.0 * (0x1p-8 + 0x1p-8 + 0x1p-16) + 2.04 * km_gamma(NACC)) * (1.0 + 0x1p-20));
     constexpr float GAM2 = (float)((1.01 * km_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
     constexpr float GDIR = (float)(km_gamma(D + 2) / (1.0 - km_gamma(D + 2)) * (1.0 + 0x1p-20));
     constexpr float RHO = (float)(1.01 * (double)(1 << G::IB) * 0x1p-23);
@@ -387,8 +389,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     const int h = lane >> 5, ln = lane & 31;
     __syncthreads();
     // The screen's A operand from the float32 centres: for centre tile t and K-step s < DS, lane (h, ln) holds
-    // the high bf16 piece of -2 c[32t + ln][h*DH + 8s + q], and K-step DS + s the low piece (the bf16 residual);
-    // K-step 2 DS carries |c|^2 (float32 of the float64 sum over dims ascending; 3e38 for padding centres, never a
+    // bf16(-2 c[32t + ln][h*DH + 8s + q]); K-step DS carries |c|^2 (float32 of the float64 sum over dims
+    // ascending; 3e38 for padding centres, never a
     // candidate and finite so packed keys stay ordered) as two bf16 pieces against a B operand of ones, so
     // |c|^2 - 2 x.c comes out of the matrix cores directly. The window needs max |c| (rounded up) and max |c|^2
     // over the real centres.
@@ -415,13 +417,11 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
             for (int q = 0; q < 8; q++) {
                 const int j = h * DH + 8 * st + q;
                 const float v = (real && j < D) ? -2.0f * Cl[cA * CS + j] : 0.0f;
-                const __bf16 vh = (__bf16)v;
-                Aop[t][st][q] = vh;
-                Aop[t][DS + st][q] = (__bf16)(v - (float)vh);
+                Aop[t][st][q] = (__bf16)v;
             }
         const float hi = (float)(__bf16)sf;
 #pragma unroll
-        for (int q = 0; q < 8; q++) Aop[t][2 * DS][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
+        for (int q = 0; q < 8; q++) Aop[t][DS][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
     }
     for (int off = 32; off > 0; off >>= 1) {
         cn_l = fmaxf(cn_l, __shfl_xor(cn_l, off));
