@@ -4,10 +4,11 @@
 // (v_mfma_f32_32x32x16_bf16: A = bf16(-2c), 32 centres x 16 dims; B = bf16(x), 16 dims x 32 rows; C = |c|^2).
 // That value is only a screen. A rigorous bound on its error, plus the error bound of the float32 direct form,
 // gives a window: every centre whose exact float32 direct-form distance could be the row's minimum has a'_c
-// inside it. Those candidates - almost always one - are rescored with the direct form in the rows loop's order
-// (core.py:263-274), ascending centre index with a strict '<', so labels and best are the rows loop's bit for
-// bit. This is the reference's tiles + margin design (core.py:333-377, 675-784) rebuilt for CDNA4: bf16 matrix
-// cores instead of fp32 simdgroup MMA, the window derived for that arithmetic, and no n x k matrix in memory.
+// inside it. A row whose window holds the screen's minimiser alone has that label, the rows loop's; the other rows
+// (uncommon) are scored against every centre by the whole wave in the rows loop's order (core.py:263-274), ascending
+// centre index with a strict '<', so labels and best are the rows loop's bit for bit. This is the reference's
+// tiles + margin design (core.py:333-377, 675-784) rebuilt for CDNA4: bf16 matrix cores instead of fp32 simdgroup
+// MMA, the window derived for that arithmetic, and no n x k matrix in memory.
 //
 // Lane layout (wave64, one 32-row tile): lane l holds row n = l & 31 of the tile and half h = l >> 5 of its
 // dims: [h*DH, h*DH + DH), DH = DP/2. MFMA K-step s (16 contraction slots) takes dims h*DH + 8s + q (q < 8) from
@@ -20,7 +21,7 @@
 // pieces (split3), so the float32 MFMA accumulators add the float32 row values themselves, rounded only by the
 // accumulation. Counts are LDS integer adds (exact, order-free). The block's inertia partial is a per-lane Kahan sum
 // of the rows' distances. With BEST every row's distance is the exact direct form (labels, best outputs); without
-// it only rows whose window holds several centres are rescored with the direct form, and the others - whose label
+// it only rows whose window holds several centres get the direct form (from the wave's scan), and the others - whose label
 // is the screen's minimiser, exactly the rows loop's label - add their distance in FMA form, which agrees with the
 // direct form to float32 rounding. At the end of its rows each wave leaves its accumulators in LDS and the block folds them
 // in wave order (Neumaier across waves) into one partial per block; the partials are reduced in a fixed order
@@ -79,21 +80,11 @@ __device__ __forceinline__ void own_halves(float va, float vb, float &h0, float 
     h0 = f32(r[0]);
     h1 = f32(r[1]);
 }
-__device__ __forceinline__ void own_halves_u(uint32_t va, uint32_t vb, uint32_t &h0, uint32_t &h1) {
-    const auto r = __builtin_amdgcn_permlane32_swap(va, vb, false, false);
-    h0 = r[0];
-    h1 = r[1];
-}
 // orders this wave's LDS accesses (every lane's earlier reads and writes before any later one)
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-// value of lane l ^ 32
-__device__ __forceinline__ float partner(float v, int lane) {
-    const auto r = __builtin_amdgcn_permlane32_swap(u32(v), u32(v), false, false);
-    return f32(lane < 32 ? r[1] : r[0]);
 }
 
 // Error-window constants. u = 2^-24 (float32 unit roundoff); gamma_m = m u / (1 - m u).
@@ -163,43 +154,6 @@ __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], flo
             m2 = vmin(m2, __builtin_amdgcn_fmed3f(m1, ka, kb));
             m1 = vmin3(m1, ka, kb);
         }
-}
-
-// Candidate bits of this lane's screen values: bit (8(v/4) + 4h + v%4) of word t is set when a[t][v] <= T2. The
-// values are compared unpacked; T2 = T + 4 RHO |T| + tiny covers the packing perturbation, so the set contains
-// every centre the packed-key test would admit. The bits shift in with v = 15 first, so bit v lands at position v;
-// a nibble-to-byte spread places them.
-template <int D, int KP>
-__device__ __forceinline__ void cand_bits(const f32x16 (&a)[Geo<D, KP>::KT], float T2, int h,
-                                          uint32_t (&w)[Geo<D, KP>::KT]) {
-    using G = Geo<D, KP>;
-#pragma unroll
-    for (int t = 0; t < G::KT; t++) {
-        // compiled code, not inline asm: the values are matrix-core results, and only the compiler's hazard
-        // tracking inserts the wait states a vector instruction needs before it may read them
-        uint32_t m = 0;
-#pragma unroll
-        for (int v = 15; v >= 0; v--) m = 2u * m + (a[t][v] <= T2 ? 1u : 0u);
-        // byte j = nibble j of the 16-bit mask
-        const uint32_t p = __builtin_amdgcn_perm(m, m, 0x01010000u);   // bytes b0, b0, b1, b1
-        const uint32_t q = ((p & 0x000f000fu) | ((p >> 4) & 0x0f000f00u));
-        w[t] = q << (4 * h);
-    }
-}
-
-template <int D, int KP>
-__device__ __forceinline__ void load_half(const float *__restrict__ X, int64_t row, int h, float (&x)[Geo<D, KP>::DH]) {
-    using G = Geo<D, KP>;
-    static_assert(D == G::DP, "rows are loaded as whole float4s");
-    const float4 *src = reinterpret_cast<const float4 *>(X + row * D + h * G::DH);
-#pragma unroll
-    for (int q = 0; q < G::DH / 4; q++) {
-        const float4 v = src[q];
-        x[4 * q] = v.x;
-        x[4 * q + 1] = v.y;
-        x[4 * q + 2] = v.z;
-        x[4 * q + 3] = v.w;
-    }
 }
 
 __device__ __forceinline__ bf16x2 as_bf2(uint32_t v) { return *reinterpret_cast<bf16x2 *>(&v); }
@@ -495,105 +449,74 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
         float T = akm + ((2.0f * E + 2.0f * GDIR * dm_up) * (1.0f + 0x1p-20f) + TINY);
         T = T + 0x1p-22f * fabsf(T);
         const bool unique = (k2 - RHO * fabsf(k2)) > T && cm < k;
-        uint32_t mw[KT];
-#pragma unroll
-        for (int t = 0; t < KT; t++) mw[t] = (t == kt && cm < k) ? (1u << (cm & 31)) : 0u;
-        // ---- rows the screen cannot settle alone: every centre inside the window (rare)
-        if (__ballot(!unique && valid) != 0) {
-            asm volatile("" ::: "memory");   // the re-reads below stay inside this branch
-            float ya[DH], yb[DH];
-            read_half<D>(buf, 0, lane, ya);
-            read_half<D>(buf, 1, lane, yb);
-            const float T2 = T + (4.0f * RHO * fabsf(T) + TINY);
-            const float Tp = partner(T2, lane);
-            const float TA = (lane < 32) ? T2 : Tp, TB = (lane < 32) ? Tp : T2;
-            uint32_t wa[KT], wb[KT];
-            {
-                bf16x8 B[DS];
-                (void)make_b<D, KP>(ya, B);
-                f32x16 a[KT];
-                screen_tile<D, KP>(B, Aop, Bone, a);
-                cand_bits<D, KP>(a, TA, h, wa);
-            }
-            {
-                bf16x8 B[DS];
-                (void)make_b<D, KP>(yb, B);
-                f32x16 a[KT];
-                screen_tile<D, KP>(B, Aop, Bone, a);
-                cand_bits<D, KP>(a, TB, h, wb);
-            }
-#pragma unroll
-            for (int t = 0; t < KT; t++) {
-                uint32_t u0, u1;
-                own_halves_u(wa[t], wb[t], u0, u1);
-                uint32_t u = u0 | u1;
-                const int lim = k - 32 * t;
-                if (lim < 32) u &= lim <= 0 ? 0u : ((1u << lim) - 1u);
-                if (!unique) mw[t] = u;
-            }
-            uint32_t any = 0;
-#pragma unroll
-            for (int t = 0; t < KT; t++) any |= mw[t];
-            if (any == 0) {   // nothing finite in the window (non-finite data): score every centre
-#pragma unroll
-                for (int t = 0; t < KT; t++) {
-                    const int lim = k - 32 * t;
-                    mw[t] = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
-                }
-            }
-        }
         float bst = 0.0f;
         uint32_t bl = unique ? (uint32_t)cm : 0u;
-        if (BEST || __ballot(!unique && valid) != 0) {
+        if (BEST) {
+            // ---- every row's exact distance to its label: the lane takes its whole row (rows the window leaves
+            // open get theirs from the scan below)
             asm volatile("" ::: "memory");
-            // ---- every lane takes its whole row
             float lo[DH], hi[DH];
 #pragma unroll
             for (int q = 0; q < DH; q++) own_halves(xa[q], xb[q], lo[q], hi[q]);
-            if (BEST || !unique) {
-                // ---- exact rescoring: the lowest candidate, then (rare) the others in ascending order, strict '<'
-                int c0 = 0;
-                {
-                    bool got = false;
+            const float *cc = Cl + (unique ? cm : 0) * CS;
+            float s = 0.0f;
 #pragma unroll
-                    for (int t = 0; t < KT; t++)
-                        if (!got && mw[t]) {
-                            c0 = 32 * t + __builtin_ctz(mw[t]);
-                            got = true;
-                        }
-                }
-                bl = (uint32_t)c0;
-                {
-                    const float *cc = Cl + c0 * CS;
-                    float s = 0.0f;
+            for (int q = 0; q < DH; q++) { const float t = lo[q] - cc[q]; s = s + t * t; }
 #pragma unroll
-                    for (int q = 0; q < DH; q++) { const float t = lo[q] - cc[q]; s = s + t * t; }
+            for (int q = 0; q < DH; q++) { const float t = hi[q] - cc[DH + q]; s = s + t * t; }
+            bst = s;
+            // the rows loop keeps best = INFINITY and label 0 when no distance compares below it (NaN)
+            if (!(s < INFINITY)) { bst = INFINITY; bl = 0; }
+        }
+        // ---- rows the window leaves open (uncommon: about 0.5 % of rows on 10M x 32, k = 64 blobs with outliers,
+        // non-finite rows always): the whole wave scores every centre of each such row in the rows loop's order
+        // (dims ascending, lane c taking centres c, c + 64, ... ascending with a strict '<'), then keeps the
+        // smallest distance and the lowest index among equal ones - the rows loop's label and best, label 0 and
+        // best +inf included when no distance compares below +inf. The row is read from the block buffer by
+        // every lane at one address (a broadcast).
+        uint64_t need = __ballot(!unique && valid);
+        if (need) {
+            asm volatile("" ::: "memory");
+            fallback += (!unique && valid) ? 1u : 0u;
+            do {
+                const int L = __builtin_ctzll(need);
+                need &= need - 1;
+                const char *rowp = buf + L * (D * 4);
+                const int swl = swz<D>(L);
+                float bv = INFINITY;
+                uint32_t bi = 0;
+                for (int c = lane; c < k; c += 64) {
+                    const float *cc = Cl + c * CS;
+                    float sc = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < DH; q++) { const float t = hi[q] - cc[DH + q]; s = s + t * t; }
-                    bst = s;
-                    // the rows loop keeps best = INFINITY and label 0 when no distance compares below it (NaN)
-                    if (!(s < INFINITY)) { bst = INFINITY; bl = 0; }
-                }
-                if (!unique) {
-                    asm volatile("" ::: "memory");
-                    mw[c0 >> 5] &= ~(1u << (c0 & 31));
-                    fallback += valid ? 1u : 0u;
-#pragma unroll
-                    for (int t = 0; t < KT; t++) {
-                        uint32_t wv = mw[t];
-                        while (wv) {
-                            const int b = __builtin_ctz(wv);
-                            wv &= wv - 1u;
-                            const int c = 32 * t + b;
-                            const float *cc = Cl + c * CS;
-                            float s = 0.0f;
-                            for (int q = 0; q < DH; q++) { const float tq = lo[q] - cc[q]; s = s + tq * tq; }
-                            for (int q = 0; q < DH; q++) { const float tq = hi[q] - cc[DH + q]; s = s + tq * tq; }
-                            if (s < bst) { bst = s; bl = (uint32_t)c; }
-                        }
+                    for (int p = 0; p < D / 4; p++) {
+                        const float4 xq = *reinterpret_cast<const float4 *>(rowp + ((p ^ swl) << 4));
+                        const float t0 = xq.x - cc[4 * p], t1 = xq.y - cc[4 * p + 1];
+                        const float t2 = xq.z - cc[4 * p + 2], t3 = xq.w - cc[4 * p + 3];
+                        sc = sc + t0 * t0;
+                        sc = sc + t1 * t1;
+                        sc = sc + t2 * t2;
+                        sc = sc + t3 * t3;
+                    }
+                    if (sc < bv) {
+                        bv = sc;
+                        bi = (uint32_t)c;
                     }
                 }
-            }
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) {
+                    const float ov = __shfl_xor(bv, off);
+                    const uint32_t oi = (uint32_t)__shfl_xor((int)bi, off);
+                    if (ov < bv || (ov == bv && oi < bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                if (lane == L) {
+                    bst = bv;
+                    bl = bi;
+                }
+            } while (need);
         }
         if (!BEST && ACCUM) {
             // inertia of the rows the screen settled alone: |x - c_m|^2 in FMA form on the half-rows each lane
