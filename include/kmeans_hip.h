@@ -114,8 +114,8 @@ int32_t km_profile_read(km_ctx *ctx, int32_t kernel, double *ms_total, int64_t *
 const char *km_kernel_name(int32_t kernel);
 
 /* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS, _MFMA or _FUSED), and the number of
- * rows in that pass the matrix-core screen could not settle with its candidate list: on the fused path (dims 16,
- * 32, 64) rows with more than one centre inside the error window, rescored against every centre in it; on the
+ * rows in that pass the matrix-core screen could not settle alone: on the fused path (dims 16, 32, 64) rows with
+ * more than one centre inside the error window (or non-finite rows), scored against every centre; on the
  * wide-row path rows that took the full scan of every centre (more than 16 centres in a half-row's window, or
  * non-finite data). 0 on the other paths. */
 int32_t km_last_path(const km_ctx *ctx);
