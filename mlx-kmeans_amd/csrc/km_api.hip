@@ -66,6 +66,7 @@ struct ProfRec {
 
 struct km_ctx {
     int device = 0;
+    km_device_info dev{256, 65536};
     hipStream_t stream = nullptr;
     std::vector<Part> parts;
     int32_t d = 0;
@@ -78,6 +79,7 @@ struct km_ctx {
     DBuf<uint16_t> ncand;
     DBuf<uint16_t> cand;
     DBuf<uint32_t> hist, counts, base, perm, over, multi;
+    DBuf<uint32_t> xmax;    // wide-row path: the largest |x|^2 over every slice (float bits)
     DBuf<float> Cb[2];      // centre buffers (k, d): pass p reads Cb[p & 1], writes Cb[(p + 1) & 1]
     DBuf<float> psum, pcomp;
     DBuf<double> tot;
@@ -162,6 +164,11 @@ extern "C" km_ctx *km_create(int32_t device) {
     if (hipSetDevice(device) != hipSuccess) return nullptr;
     km_ctx *c = new km_ctx();
     c->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+        if (prop.multiProcessorCount > 0) c->dev.cus = prop.multiProcessorCount;
+        if (prop.sharedMemPerBlock > 0) c->dev.lds_max = (size_t)prop.sharedMemPerBlock;
+    }
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return nullptr;
@@ -211,6 +218,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->perm.release();
     c->over.release();
     c->multi.release();
+    c->xmax.release();
     c->red.release();
     c->labels.release();
     c->best.release();
@@ -319,9 +327,9 @@ static bool big_ok(const km_ctx *c, int k) {
 // Returns the kernel family for this pass (FAM_*), or -1 when an explicit path does not serve the shape.
 static int choose_path(km_ctx *c, int k, int path, km_mfma_plan *mp) {
     const bool al = parts_aligned(c);
-    *mp = km_plan_mfma(c->n, c->d, k);
+    *mp = km_plan_mfma(c->dev, c->n, c->d, k);
     if (!al) mp->ok = 0;
-    const bool lowd_ok = km_plan_lowd(c->n, c->d, k, al).ok != 0;
+    const bool lowd_ok = km_plan_lowd(c->dev, c->n, c->d, k, al).ok != 0;
     const bool wide_ok = big_ok(c, k);
     if (path == KM_PATH_ROWS) return FAM_ROWS;
     if (path == KM_PATH_MFMA) return mp->ok ? FAM_MFMA_FUSED : wide_ok ? FAM_BIG : -1;
@@ -375,11 +383,13 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     const float *Cin = c->Cb[pass & 1].p;
     int64_t max_rows = 0;
     int max_nb = 0;
+    bool built = false;
     for (auto &p : c->parts) {
         const km_big_plan bp = km_plan_big(p.rows, d, k);
         max_rows = std::max(max_rows, p.rows);
         max_nb = std::max(max_nb, bp.nb);
         if (!p.x16 || p.x16_ds != bp.DS) {
+            built = true;
             if (p.x16) (void)hipFree(p.x16);
             if (p.xsq) (void)hipFree(p.xsq);
             p.x16 = nullptr;
@@ -389,6 +399,12 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
             HIPCHK(c, launch(c, KK_BIG_PREP, [&] { return km_launch_big_rows(bp, p.X, p.rows, d, p.x16, p.xsq, c->stream); }));
             p.x16_ds = bp.DS;
         }
+    }
+    if (built) {   // a slice's row norms are new: the largest |x|^2 over all slices again
+        HIPCHK(c, c->xmax.ensure(1));
+        HIPCHK(c, hipMemsetAsync(c->xmax.p, 0, sizeof(uint32_t), c->stream));
+        for (auto &p : c->parts)
+            HIPCHK(c, launch(c, KK_BIG_PREP, [&] { return km_launch_big_xmax(p.xsq, p.rows, c->xmax.p, c->stream); }));
     }
     const km_big_plan bp0 = km_plan_big(max_rows, d, k);
     HIPCHK(c, c->cop.ensure(km_big_cop_elems(bp0)));
@@ -425,8 +441,8 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
                                              c->stream);
             }));
         HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
-            return km_launch_big_screen(bp, mode, p.x16, p.xsq, p.rows, d, c->cop.p, c->bmax.p, k, c->ncand.p,
-                                        c->cand.p, c->over.p, c->multi.p, c->ctl, stop, c->stream);
+            return km_launch_big_screen(bp, mode, p.x16, p.xsq, c->xmax.p, p.rows, d, c->cop.p, c->bmax.p, k,
+                                        c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl, stop, c->stream);
         }));
         HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {
             return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->multi.p,
@@ -467,7 +483,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         size_t total_rb = 0;
         std::vector<km_mfma_plan> plans;
         for (auto &p : c->parts) {
-            plans.push_back(km_plan_mfma(p.rows, d, k));
+            plans.push_back(km_plan_mfma(c->dev, p.rows, d, k));
             total_rb += plans.back().nrb;
         }
         int r = ensure_pass_buffers(c, k, total_rb, false);
@@ -493,7 +509,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         std::vector<km_lowd_plan> plans;
         const bool al = parts_aligned(c);
         for (auto &p : c->parts) {
-            plans.push_back(km_plan_lowd(p.rows, d, k, al));
+            plans.push_back(km_plan_lowd(c->dev, p.rows, d, k, al));
             total_rb += plans.back().nrb;
         }
         int r = ensure_pass_buffers(c, k, total_rb, false);
@@ -766,7 +782,7 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
             c->ctl_h->stop = c->ctl_h->done;
             if ((r = write_control(c))) return r;
         }
-        if (c->ctl_h->done) break;
+        if (c->ctl_h->done || !std::isfinite(c->ctl_h->inertia)) break;
     }
     if (C_out)
         HIPCHK(c, hipMemcpyAsync(C_out, c->Cb[c->ctl_h->iter & 1].p, (size_t)k * c->d * sizeof(float),

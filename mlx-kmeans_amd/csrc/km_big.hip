@@ -30,6 +30,7 @@ static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
 static constexpr int KB_SLICE = 16;       // A-operand K-steps per LDS slice (16 KB)
 static constexpr int KB_WAVES = 4;        // waves per screen block (32 rows each)
 static constexpr int KB_OVER = 0xffff;    // ncand value: scan every centre
+static constexpr double KB_APPROX_LIMIT = 65504.0 / 4;   // the reference's APPROX_FP16_LIMIT (core.py:1035)
 
 __host__ __device__ constexpr double kb_gamma(int m) {
     return m * 5.9604644775390625e-08 / (1.0 - m * 5.9604644775390625e-08);
@@ -105,6 +106,16 @@ __global__ __launch_bounds__(256) void k_big_xsq(const float *__restrict__ X, in
         xn[2 * row] = ok ? (float)(s * (1.0 + 0x1p-20)) : INFINITY;
         xn[2 * row + 1] = ok ? (float)(sqrt(r) * (1.0 + 0x1p-20)) : INFINITY;
     }
+}
+
+// The largest |x|^2 of a slice (float bits of the non-negative xn[2 row], +inf included) into *xmax by an
+// integer maximum: for non-negative floats the bit patterns order as the values do.
+__global__ __launch_bounds__(256) void k_big_xmax(const float *__restrict__ xn, int64_t n, uint32_t *__restrict__ xmax) {
+    uint32_t m = 0;
+    for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < n; r += (int64_t)gridDim.x * 256)
+        m = max(m, kb_u32(xn[2 * r]));
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+    if ((threadIdx.x & 63) == 0) atomicMax(xmax, m);
 }
 
 // ------------------------------------------------------------------ centres (per pass)
@@ -229,14 +240,19 @@ template <int DS>
 __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
-    int approx, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
-    uint32_t *__restrict__ multi, km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
+    int approx, const uint32_t *__restrict__ xmax, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand,
+    uint32_t *__restrict__ over, uint32_t *__restrict__ multi, km_control *__restrict__ ctl,
+    const int32_t *__restrict__ stop) {
     constexpr int DP = 16 * DS, AK = DS + 1, NACC = DP + 2;
     constexpr float GACC = (float)(2.04 * kb_gamma(NACC) * (1.0 + 0x1p-20));
     constexpr float GAM2 = (float)((1.01 * kb_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
     constexpr float FLUSH = (float)0x1p-119;
     constexpr float TINY = (float)((DP + 2) * 0x1p-118);
     if (stop && *stop) return;
+    // Approximate mode only while this pass's centres pass the reference's half-precision guard (core.py:1055-1058):
+    // sqrt(max |x|^2 max |c|^2) < 65504 / 4, from the data's largest |x|^2 (rounded up, +inf if any row is not
+    // finite) and the largest |c|^2 of the centres. Otherwise the pass is exact.
+    if (approx) approx = sqrt((double)kb_f32(*xmax) * (double)maxes[1]) < KB_APPROX_LIMIT;
     extern __shared__ float lds[];
     char *ring = reinterpret_cast<char *>(lds);   // two slices of at most KB_SLICE K-steps, 1 KB each
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -380,7 +396,9 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (!real_row) return;
-    const int cnt_o = (int)kb_f32u(kb_partner(kb_u32f((uint32_t)cnt), lane));
+    // The other half-row's count, or KB_HALF + 1 when its list overflowed: a lane's count never exceeds KB_HALF
+    // (the final filter only lowers it), so the overflow has to travel as its own value.
+    const int cnt_o = (int)kb_f32u(kb_partner(kb_u32f((uint32_t)(spill ? KB_HALF + 1 : cnt)), lane));
     const bool spill_o = cnt_o > KB_HALF;
     if (h != 0) return;
     int code;
@@ -862,8 +880,8 @@ __global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__rest
 // ------------------------------------------------------------------ planning and launch
 
 typedef void (*screen_fn)(const uint16_t *, const float *, int64_t, int, const uint16_t *, const float *, int, int,
-                          int, float, int, uint16_t *, uint16_t *, uint32_t *, uint32_t *, km_control *,
-                          const int32_t *);
+                          int, float, int, const uint32_t *, uint16_t *, uint16_t *, uint32_t *, uint32_t *,
+                          km_control *, const int32_t *);
 
 static screen_fn kb_screen_for(int DS) {
     switch (DS) {
@@ -916,6 +934,12 @@ hipError_t km_launch_big_rows(const km_big_plan &pl, const float *X, int64_t n, 
     return hipGetLastError();
 }
 
+hipError_t km_launch_big_xmax(const float *xsq, int64_t n, uint32_t *xmax, hipStream_t s) {
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_big_xmax, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, s, xsq, n, xmax);
+    return hipGetLastError();
+}
+
 hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, int d, float *csq, float *cn,
                                  uint16_t *Cop, float *maxes, km_control *ctl, const int32_t *stop, hipStream_t s) {
     hipLaunchKernelGGL(k_big_cnorm, dim3((unsigned)((pl.kpad + 3) / 4)), dim3(256), 0, s, C, k, pl.kpad, d, csq, cn,
@@ -928,16 +952,20 @@ hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, i
     return hipGetLastError();
 }
 
-hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
-                                int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
-                                uint32_t *over, uint32_t *multi, km_control *ctl, const int32_t *stop, hipStream_t s) {
+hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq,
+                                const uint32_t *xmax, int64_t n, int d, const uint16_t *Cop, const float *maxes, int k,
+                                uint16_t *ncand, uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
+                                const int32_t *stop, hipStream_t s) {
     screen_fn fn = kb_screen_for(pl.DS);
     if (!fn) return hipErrorInvalidValue;
     const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
     const unsigned blocks = (unsigned)((pl.ntiles + KB_WAVES - 1) / KB_WAVES);
+    // exact=False approximates from 64 dims, and only under the half-precision guard (checked in the kernel);
+    // below 64 dims the reference's dispatch runs its exact kernels (core.py:2036-2042)
+    const int approx = (mode == KM_APPROX && d >= KM_APPROX_MIN_DIMS) ? 1 : 0;
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), 2 * KB_SLICE * 1024 + KB_WAVES * KB_HALF * 64 * 4, s, X16T,
-                       xsq, n, d, Cop, maxes, k,
-                       pl.nchunks, pl.ib, rho, mode == KM_APPROX ? 1 : 0, ncand, cand, over, multi, ctl, stop);
+                       xsq, n, d, Cop, maxes, k, pl.nchunks, pl.ib, rho, approx, xmax, ncand, cand, over, multi, ctl,
+                       stop);
     return hipGetLastError();
 }
 

@@ -315,7 +315,8 @@ __device__ void pass_stats(const double *tot, int k, int d, float *Cnext, km_con
         ctl->need_reloc = need_reloc;
         ctl->done = done;
         ctl->iter = pass + 1;
-        ctl->stop = (done || need_reloc) ? 1 : 0;
+        // a non-finite inertia (NaN or overflowing data) ends the loop at once: the caller explains it
+        ctl->stop = (done || need_reloc || !isfinite(inertia)) ? 1 : 0;
     }
     if (ne > 0 && !need_reloc) {
         for (int cc = 0; cc < k; cc++) {

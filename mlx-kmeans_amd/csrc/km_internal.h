@@ -25,7 +25,8 @@ __device__ __forceinline__ void lds_dma16(const void *src, lds_vptr dst) {
 // iterations can run back to back with no host round trip.
 struct km_control {
     int32_t iter;        // passes completed in the current loop (the update stage of pass p sets it to p+1)
-    int32_t stop;        // set when no further pass may run: converged, or an empty cluster needs relocating
+    int32_t stop;        // set when no further pass may run: converged, an empty cluster needs relocating, or
+                         // the inertia came out non-finite
     int32_t done;        // |prev - inertia| <= tol * prev held at the last completed pass
     int32_t need_reloc;  // the last completed pass left clusters empty while some row had best > 0
     int32_t n_empty;     // empty clusters in the last completed pass
@@ -36,6 +37,12 @@ struct km_control {
     double prev;         // inertia of the pass before it
     double tol;
     uint64_t fallback_rows;  // rows the MFMA screen left to a full rescoring, summed over passes
+};
+
+// What the planners need to know of the device a context runs on (read once, in km_create).
+struct km_device_info {
+    int cus;          // compute units
+    size_t lds_max;   // LDS bytes one workgroup may use
 };
 
 // Kernel ids for timing (order fixed; names in km_kernel_names).
@@ -108,7 +115,7 @@ struct km_mfma_plan {
     int waves;       // waves per block
     size_t lds;
 };
-km_mfma_plan km_plan_mfma(int64_t n, int d, int k);
+km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k);
 // want_best: every row's exact direct-form distance (labels/best outputs); without it, rows the screen settles
 // alone add an FMA-form distance to the pass inertia (their labels are exact either way).
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
@@ -124,7 +131,7 @@ struct km_lowd_plan {
     size_t lds;      // dynamic LDS bytes
     int lsh;         // the wave keeps 64 >> lsh tile columns; 1 << lsh lanes take turns on each
 };
-km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned);
+km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned);
 hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int d, const float *C, int k,
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s);
@@ -147,9 +154,14 @@ hipError_t km_launch_big_rows(const km_big_plan &pl, const float *X, int64_t n, 
                               hipStream_t s);
 hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, int d, float *csq, float *cn,
                                  uint16_t *Cop, float *maxes, km_control *ctl, const int32_t *stop, hipStream_t s);
-hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq, int64_t n,
-                                int d, const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
-                                uint32_t *over, uint32_t *multi, km_control *ctl, const int32_t *stop, hipStream_t s);
+// xmax: the largest |x|^2 over every slice (float bits), for the approximate mode's half-precision guard
+hipError_t km_launch_big_xmax(const float *xsq, int64_t n, uint32_t *xmax, hipStream_t s);
+// KM_APPROX approximates from KM_APPROX_MIN_DIMS dims while sqrt(max |x|^2 max |c|^2) < 65504 / 4; exact otherwise
+#define KM_APPROX_MIN_DIMS 64
+hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq,
+                                const uint32_t *xmax, int64_t n, int d, const uint16_t *Cop, const float *maxes, int k,
+                                uint16_t *ncand, uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
+                                const int32_t *stop, hipStream_t s);
 // lite: the pass returns no per-row distances; single-candidate rows take their label without one
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,

@@ -434,8 +434,6 @@ static lowd_fn g_lowd[2][2][17] = {{KM_LOWD_FNS(false, 0), KM_LOWD_FNS(false, KM
                                    {KM_LOWD_FNS(true, 0), KM_LOWD_FNS(true, KM_LOWD_SHARED_LSH)}};
 #undef KM_LOWD_FNS
 
-static int g_lowd_cus = 0;
-
 static int lowd_rows_per_iter(int d) { return 64 * (d <= 8 ? 8 : 4); }
 
 // The screen costs d + 3 operations per centre and row against the direct form's 3d + 3, plus a per-row window
@@ -443,19 +441,12 @@ static int lowd_rows_per_iter(int d) { return 64 * (d <= 8 ? 8 : 4); }
 // (20M rows: d = 4, k = 32 -21 %; d = 2, k = 48 -15 %) and not below (d = 4, k = 12 +5 %; d = 8, k = 8 +1 %).
 static bool lowd_screen(int k) { return k >= 24; }
 
-km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
+km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned) {
     km_lowd_plan pl{};
     if (d < 1 || d > 16 || k < 1 || n < 1) return pl;
     if ((int64_t)k * (d + 2) > KM_LOWD_MAX_KW) return pl;
     if ((d % 2 == 0) && !aligned) return pl;   // vector row loads need 8/16-byte aligned rows
     const bool scr = lowd_screen(k);
-    if (g_lowd_cus == 0) {
-        int dev = 0;
-        hipDeviceProp_t prop;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-            g_lowd_cus = prop.multiProcessorCount;
-        if (g_lowd_cus <= 0) g_lowd_cus = 256;
-    }
     // private tile columns unless sharing them lets more waves reside (LDS- rather than register-bound)
     int occs[2] = {0, 0};
     for (int h = 0; h < 2; h++) {
@@ -474,7 +465,7 @@ km_lowd_plan km_plan_lowd(int64_t n, int d, int k, bool aligned) {
     const size_t lds = km_lowd_lds(d, k, scr, lsh);
     const int64_t unit = lowd_rows_per_iter(d);
     const int64_t units = (n + unit - 1) / unit;
-    int64_t nrb = (int64_t)g_lowd_cus * occ;
+    int64_t nrb = (int64_t)dev.cus * occ;
     if (nrb > units) nrb = units;
     if (nrb < 1) nrb = 1;
     int64_t rbs = (n + nrb - 1) / nrb;

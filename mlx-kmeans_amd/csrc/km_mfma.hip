@@ -741,29 +741,16 @@ static const fused_entry *find_fused(int d, int k) {
     return nullptr;
 }
 
-static int g_cus = 0;
-static size_t g_lds_max = 0;
-
-km_mfma_plan km_plan_mfma(int64_t n, int d, int k) {
+km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k) {
     km_mfma_plan pl{};
     const fused_entry *fe = find_fused(d, k);
     if (!fe || n < 1) return pl;
-    if (g_cus == 0) {
-        int dev = 0;
-        hipDeviceProp_t prop;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess) {
-            g_cus = prop.multiProcessorCount;
-            g_lds_max = (size_t)prop.sharedMemPerBlock;
-        }
-        if (g_cus <= 0) g_cus = 256;
-        if (g_lds_max == 0) g_lds_max = 65536;
-    }
     int waves = 4;
     size_t lds = lds_for(d, fe->kp, 4);
-    if (lds > g_lds_max) {
+    if (lds > dev.lds_max) {
         waves = 2;
         lds = lds_for(d, fe->kp, 2);
-        if (lds > g_lds_max) return pl;
+        if (lds > dev.lds_max) return pl;
     }
     fused_fn fn = waves == 4 ? fe->acc4 : fe->acc2;
     if (lds > 65536) {
@@ -779,7 +766,7 @@ km_mfma_plan km_plan_mfma(int64_t n, int d, int k) {
     pl.dpad = (d + 15) / 16 * 16;
     pl.lds = lds;
     pl.waves = waves;
-    const int64_t slots = (int64_t)g_cus * occ;
+    const int64_t slots = (int64_t)dev.cus * occ;
     const int64_t unit = 64 * waves;
     const int64_t units = (n + unit - 1) / unit;
     int64_t nrb = units < slots ? units : slots;

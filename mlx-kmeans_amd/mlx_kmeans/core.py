@@ -22,7 +22,8 @@ import numpy as np
 from . import _lib
 
 SLICE_ROWS = 100_000_000                # rows per slice that KMeans cuts its input into
-PART_MAX_ELEMENTS = 2**32 - 1           # elements per slice (the reference's uint32 offsets; kept for callers)
+PART_MAX_ELEMENTS = 2**32 - 1           # elements per slice: the reference's limit (its kernels' uint32 offsets),
+                                        # refused above it as the reference does (core.py:2028-2032)
 
 # the reference's `method` names -> this engine's paths. "rows" is the direct-form scan; the matrix-core screen
 # plays the part of the reference's "tiles"/"tiles1"; the others are reference-internal variants that map onto
@@ -89,6 +90,13 @@ def _validate_parts(parts):
     bad = [p.shape[1] for p in parts if p.shape[1] != d]
     if bad:
         raise ValueError(f"slices have {bad[0]} and {d} columns; every slice needs the same features")
+    # one slice holds at most PART_MAX_ELEMENTS values, as in the reference (core.py:2028-2032); KMeans cuts its
+    # input into slices of slice_rows(dims) rows itself
+    big = [tuple(p.shape) for p in parts if int(p.shape[0]) * int(p.shape[1]) > PART_MAX_ELEMENTS]
+    if big:
+        raise ValueError(f"a slice of shape {big[0]} has more than {PART_MAX_ELEMENTS:,} elements, the limit of one "
+                         f"slice (the reference addresses a slice with 32-bit offsets); pass the data as a list of "
+                         f"slices of at most slice_rows(dims) = {slice_rows(d):,} rows (KMeans does this itself)")
 
 
 def _context(parts, C, method="auto"):

@@ -141,14 +141,27 @@ def lloyd_step(X, C, variant=VARIANT_A1):
     return C_new, inertia, n_empty, labels, best, tot
 
 
-def fit_from(X, C0, max_iter, tol=0.0):
-    """KMeans._one_run's loop (estimator.py:136-150) from given starting centres, then the final scoring
-    pass on the returned centres (estimator.py:201-204) -> (C, inertia_final, n_iter, labels)."""
+def normalise(C):
+    """Spherical k-means' renormalisation (estimator.py:127-130): each centre over its float32 length, a zero
+    centre left as is."""
+    C = _f32(C)
+    n = np.linalg.norm(C, axis=1, keepdims=True)
+    return (C / np.where(n > 0, n, 1)).astype(np.float32)
+
+
+def fit_from(X, C0, max_iter, tol=0.0, spherical=False):
+    """KMeans._one_run's loop (estimator.py:132-150) from given starting centres - with spherical=True the
+    starting centres and every step's centres renormalised - then the final scoring pass on the returned
+    centres (estimator.py:201-204) -> (C, inertia_final, n_iter, labels)."""
     C = _f32(C0).copy()
+    if spherical:
+        C = normalise(C)
     prev = None
     it = 0
     for it in range(max_iter):
         C, inertia, _, _, _, _ = lloyd_step(X, C)
+        if spherical:
+            C = normalise(C)
         if prev is not None and abs(prev - inertia) <= tol * prev:
             break
         prev = inertia

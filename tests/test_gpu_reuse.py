@@ -89,3 +89,51 @@ def test_model_npz_round_trip_predicts_the_same(tmp_path):
     loaded = KMeans.from_centers(z["centers"])
     assert np.array_equal(loaded.predict(Xn), m.predict(Xn))
     assert np.array_equal(loaded.predict(X), m.labels_)
+
+
+@pytest.mark.parametrize("d,k", [(32, 48), (8, 12), (96, 64)])
+def test_spherical_fit_matches_oracle_loop(d, k):
+    """spherical=True (estimator.py:132-150): the starting centres and every step's centres renormalised. The
+    engine's device loop from the k-means++ start against the oracle's restatement of the loop from the same
+    start, on L2-normalised rows: same iteration count under the default tol, centres within 1e-5, labels_ the
+    oracle's assignment to the returned centres, and every returned centre of unit length."""
+    from mlx_kmeans import KMeans, core
+    rng = np.random.default_rng(50 + d + k)
+    n = 30_000
+    cen = rng.standard_normal((k, d))
+    X = cen[rng.integers(0, k, n)] + 0.25 * rng.standard_normal((n, d))
+    X = (X / np.linalg.norm(X, axis=1, keepdims=True)).astype(np.float32)
+    say(f"[gpu] spherical fit d={d} k={k}")
+    m = KMeans(n_clusters=k, max_iter=40, random_state=3, spherical=True).fit(X)
+    C0 = core.kmeans_pp_init([X], n, k, np.random.default_rng(3))
+    C_ref, inertia_ref, it_ref, _ = oracle.fit_from(X, C0, 40, tol=1e-4, spherical=True)
+    assert m.n_iter_ == it_ref
+    assert float(np.max(np.abs(m.cluster_centers_.astype(np.float64) - C_ref))) <= 1e-5
+    np.testing.assert_allclose(np.linalg.norm(m.cluster_centers_.astype(np.float64), axis=1), 1.0, atol=1e-6)
+    ol, ob = oracle.assign(X, m.cluster_centers_)
+    assert np.array_equal(m.labels_, ol.astype(np.int64))
+    assert abs(m.inertia_ - float(ob.astype(np.float64).sum())) <= 1e-5 * m.inertia_
+    assert abs(m.inertia_ - inertia_ref) <= 1e-4 * inertia_ref
+
+
+def test_verbose_fit_prints_each_iteration_and_matches(capsys):
+    """verbose=True runs the loop one lloyd_step at a time and prints "iter i: inertia ..." per iteration
+    (estimator.py:143-144); the fit is the device loop's bit for bit, and with n_init > 1 each start's line
+    (estimator.py:205-207) follows."""
+    from mlx_kmeans import KMeans
+    rng = np.random.default_rng(9)
+    n, d, k = 20_000, 16, 24
+    cen = rng.uniform(-5, 5, size=(k, d))
+    X = (cen[rng.integers(0, k, n)] + rng.standard_normal((n, d))).astype(np.float32)
+    say("[gpu] verbose fit")
+    quiet = KMeans(n_clusters=k, max_iter=30, random_state=1, n_init=2).fit(X)
+    capsys.readouterr()
+    loud = KMeans(n_clusters=k, max_iter=30, random_state=1, n_init=2, verbose=True).fit(X)
+    out = capsys.readouterr().out.splitlines()
+    iters = [ln for ln in out if ln.startswith("iter ")]
+    starts = [ln for ln in out if ln.startswith("start ")]
+    assert len(starts) == 2 and starts[0].startswith("start 1/2: inertia ")
+    assert iters and iters[0].startswith("iter 1: inertia ")
+    assert np.array_equal(loud.cluster_centers_, quiet.cluster_centers_)
+    assert loud.n_iter_ == quiet.n_iter_ and loud.inertia_ == quiet.inertia_
+    assert np.array_equal(loud.labels_, quiet.labels_)

@@ -55,6 +55,22 @@ def test_core_argument_errors():
         core.kmeans([X], 20, 2, 5, 0.0, 0, backend="numpy")
 
 
+def test_slice_element_limit(monkeypatch):
+    """The reference's limit of one slice (tests/reuse.py:114-122): KMeans cuts an input over the limit into
+    slices of slice_rows(dims) rows, and a single slice over it given to the core functions is refused with the
+    reference's "32-bit" message before any device work."""
+    from mlx_kmeans import KMeans, core
+    monkeypatch.setattr(core, "PART_MAX_ELEMENTS", 1_000_000)
+    parts = KMeans._parts(np.zeros((2500, 1000), np.float32))
+    assert len(parts) == 3 and sum(len(p) for p in parts) == 2500
+    big = [np.zeros((2500, 1000), np.float32)]
+    C = np.zeros((8, 1000), np.float32)
+    for call in (lambda: core.assign_mlx(big, C), lambda: core.lloyd_step(big, C), lambda: core._gpu_pass(big, C),
+                 lambda: core.DeviceData(big)):
+        with pytest.raises(ValueError, match="32-bit"):
+            call()
+
+
 def test_synthetic_workloads_small():
     from mlx_kmeans import synthetic
     w = synthetic.blobs_d32(n=3000)

@@ -217,3 +217,42 @@ def test_label_distances_pinned(oracle):
     assert np.array_equal(oracle.distances_to(Xf, Cf, labels).view(np.uint32), best.view(np.uint32))
     with pytest.raises(ValueError):
         oracle.distances_to(Xf, Cf, np.full(4000, 50, np.uint32))
+
+
+def test_kmeans_simple_pass_pinned(oracle):
+    """kmeans_simple.py:45-78 restated: on integer-valued rows around well-separated integer centres every float32
+    step is exact (products, sums below 2^24 per chunk), so its expanded-form argmin is the rows loop's label and
+    its totals are the closed form: counts = bincount(labels), sums = np.add.at in float64, error = the sum of the
+    exact distances. A sign slip in the expanded form (|c|^2 + 2 x.c) gives other labels, which the same check
+    catches."""
+    rng = np.random.default_rng(12)
+    k, d, n = 9, 6, 50_000
+    C = (rng.integers(-4, 5, size=(k, d)) * 40).astype(np.float32)
+    lab = rng.integers(0, k, n)
+    X = (C[lab] + rng.integers(-3, 4, size=(n, d))).astype(np.float32)
+    sums, counts, err = oracle.kmeans_simple_pass(X, C, chunk=7_919)
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(ol, lab.astype(np.uint32))
+    assert np.array_equal(counts, np.bincount(ol, minlength=k).astype(np.float64))
+    ref = np.zeros((k, d))
+    np.add.at(ref, ol, X.astype(np.float64))
+    assert np.array_equal(sums, ref)
+    assert err == float(ob.astype(np.float64).sum())
+    wrong = (C * C).sum(1)[None, :] + 2 * (X @ C.T)
+    assert not np.array_equal(wrong.argmin(1), ol)
+
+
+def test_normalise_pinned(oracle):
+    """Spherical renormalisation (estimator.py:127-130): within one float32 rounding of the float64 unit vector,
+    a zero centre left at zero, and a centre already of unit length (a power-of-two axis vector) unchanged."""
+    rng = np.random.default_rng(13)
+    C = (rng.standard_normal((50, 33)) * rng.uniform(0.01, 100, (50, 1))).astype(np.float32)
+    C[7] = 0.0
+    C[8] = 0.0
+    C[8, 5] = 1.0
+    N = oracle.normalise(C)
+    C64 = C.astype(np.float64)
+    nrm = np.linalg.norm(C64, axis=1, keepdims=True)
+    want = np.where(nrm > 0, C64 / np.where(nrm > 0, nrm, 1), 0.0)
+    assert np.all(np.abs(N.astype(np.float64) - want) <= 4 * 2.0**-24 * np.maximum(np.abs(want), 2.0**-30))
+    assert np.all(N[7] == 0.0) and np.array_equal(N[8], C[8])
