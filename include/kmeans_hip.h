@@ -106,6 +106,21 @@ int32_t km_fit(km_ctx *ctx, const float *C0, int32_t k, int32_t max_iter, double
 int32_t km_seed_pp(km_ctx *ctx, int32_t k, const int64_t *sample, int64_t m, int64_t first, const uint64_t *seeds,
                    float *C_out);
 
+/* No counterpart in the reference: an allocation-free km_pass for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). One exact assignment pass over
+ * device rows X (rows x dims float32, row-major) with device centres C (k x dims): totals (device, k x (dims + 2)
+ * float64, the km_pass layout), labels (device uint32 per row) and best (device float32 per row) - all required -
+ * get km_pass's results (labels and best the same bits; totals from the same kernel family, summed over a
+ * number of row blocks that fits the scratch). Launches on `stream` (a hipStream_t; NULL is the null stream) and
+ * returns without waiting. It allocates nothing: its workspaces are the library's static device scratch array,
+ * 32 MiB per device, which every call on that device shares and which keeps the last call's contents - calls that
+ * overlap on one device race. Shapes whose partials would not fit it even as a single block (16 bytes per entry:
+ * k * (dims + 2) above about 2.09 million) are refused with KM_EINVAL before anything is launched. The wide-row path (16 < dims <= 768 in
+ * km_pass) needs a bf16 copy of the rows and is not used: those shapes run the rows path. ctx supplies the
+ * device, the scratch address and the error message; its own data and buffers are not touched. */
+int32_t km_pass_noalloc(km_ctx *ctx, const float *X, int64_t rows, int32_t dims, const float *C, int32_t k,
+                        double *totals, uint32_t *labels, float *best, void *stream);
+
 /* Kernel timing with HIP events on the context's stream. km_profile(ctx, 1) clears and starts recording;
  * km_profile_read gives, for kernel id `kernel`, the summed milliseconds and launch count so far.
  * km_kernel_name(id) names an id ("" past the last); ids are stable within one build. */

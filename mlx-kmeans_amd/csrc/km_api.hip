@@ -18,7 +18,6 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <string>
 #include <vector>
 
 #define KM_ABI_VERSION 1
@@ -71,7 +70,7 @@ struct km_ctx {
     std::vector<Part> parts;
     int32_t d = 0;
     int64_t n = 0;
-    std::string err;
+    char err[1024] = {0};   // message of the last failure (a fixed buffer: reporting allocates nothing)
     int32_t last_path = 0;
     int last_family = FAM_NONE;
     DBuf<uint16_t> cop;     // wide-row path: bf16 centre operands
@@ -92,6 +91,7 @@ struct km_ctx {
     DBuf<char> pp_ws;           // k-means++: the rounds' workspace
     km_control *ctl = nullptr;    // device
     km_control *ctl_h = nullptr;  // pinned host mirror
+    unsigned char *scratch = nullptr;   // device address of this device's copy of `scratch` (km_pass_noalloc)
     bool prof = false;
     std::vector<ProfRec> recs;
     std::vector<hipEvent_t> pool;
@@ -100,12 +100,11 @@ struct km_ctx {
 };
 
 static int fail(km_ctx *c, int code, const char *fmt, ...) {
-    char buf[1024];
+    if (!c) return code;
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    vsnprintf(c->err, sizeof c->err, fmt, ap);
     va_end(ap);
-    if (c) c->err = buf;
     return code;
 }
 
@@ -156,6 +155,15 @@ static void harvest(km_ctx *c) {
     c->recs.clear();
 }
 
+// ------------------------------------------------------------------ the allocation-free pass's scratch
+//
+// km_pass_noalloc works in this array only: its control block, per-block partials and range sums. Every device
+// the library runs on holds its own copy until the process ends; km_create looks up the copy's device address
+// with that device current and keeps it in the context (the array's name in host code is a host-side stand-in,
+// not a device address). Calls that overlap on one device share the array and race.
+#define KM_SCRATCH_BYTES ((size_t)32 << 20)
+static __device__ __align__(256) unsigned char scratch[KM_SCRATCH_BYTES];
+
 // ------------------------------------------------------------------ context and data
 
 extern "C" km_ctx *km_create(int32_t device) {
@@ -181,6 +189,9 @@ extern "C" km_ctx *km_create(int32_t device) {
         return nullptr;
     }
     memset(c->ctl_h, 0, sizeof(km_control));
+    // this device's copy of the allocation-free pass's scratch (the device is current here)
+    void *sp = nullptr;
+    if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) c->scratch = (unsigned char *)sp;
     return c;
 }
 
@@ -237,7 +248,7 @@ extern "C" void km_destroy(km_ctx *c) {
     delete c;
 }
 
-extern "C" const char *km_last_error(const km_ctx *c) { return c ? c->err.c_str() : "no context"; }
+extern "C" const char *km_last_error(const km_ctx *c) { return c ? c->err : "no context"; }
 
 static int add_part(km_ctx *c, const float *X, int64_t rows, int32_t where) {
     if (!X) return fail(c, KM_EINVAL, "data pointer is null");
@@ -841,6 +852,150 @@ extern "C" int32_t km_seed_pp(km_ctx *c, int32_t k, const int64_t *sample, int64
     HIPCHK(c, hipMemcpyAsync(C_out, c->pp_C.p, (size_t)k * d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     harvest(c);
+    return KM_OK;
+}
+
+// ------------------------------------------------------------------ one pass without allocation
+//
+// The pass of km_pass for device rows and device centres, with every workspace carved out of the context's
+// scratch (a control block, per-block partials, range sums) and the results written to the caller's device
+// buffers, all on the caller's stream: no allocation, no host copy, no synchronisation. The exact kernel families
+// of km_pass serve it, except the wide-row path (its bf16 copy of the rows is as large as the data): shapes it
+// would take run the rows path, whose labels and best are the same bits.
+
+// Zero n words (a kernel, not hipMemsetAsync: a caller may capture the stream into a graph).
+__global__ __launch_bounds__(256) void k_na_clear(uint32_t *__restrict__ p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+// totals[c][1] = tot2[c][1]: the per-cluster best sums of the [count, best] accumulation.
+__global__ __launch_bounds__(256) void k_na_best_col(const double *__restrict__ tot2, int k, int w,
+                                                     double *__restrict__ totals) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c < k) totals[(int64_t)c * w + 1] = tot2[(int64_t)c * 2 + 1];
+}
+
+// Bump allocator over the scratch array: 256-byte aligned pieces, false once it is exhausted.
+struct ScratchCarve {
+    unsigned char *base;
+    size_t used, cap;
+    template <class T>
+    bool take(T **p, size_t count) {
+        const size_t bytes = (count * sizeof(T) + 255) / 256 * 256;
+        if (used + bytes > cap) return false;
+        *p = reinterpret_cast<T *>(base + used);
+        used += bytes;
+        return true;
+    }
+};
+
+// Bytes of scratch the reduce + finish of nrb partials of kw entries use (partials included).
+static size_t na_reduce_bytes(int nrb, int64_t kw) {
+    const int S = km_reduce_splits(nrb, kw);
+    auto r = [](size_t b) { return (b + 255) / 256 * 256; };
+    return 2 * r((size_t)nrb * kw * sizeof(float)) + r((size_t)S * kw * sizeof(double));
+}
+
+// Largest block count whose partials + range sums fit `avail` bytes (at least 1, or 0 if even one does not).
+static int64_t na_max_blocks(size_t avail, int64_t kw) {
+    int64_t lo = 0, hi = 1 << 20;
+    while (lo < hi) {   // largest nrb with na_reduce_bytes(nrb) <= avail
+        const int64_t mid = (lo + hi + 1) / 2;
+        if (na_reduce_bytes((int)mid, kw) <= avail) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+extern "C" int32_t km_pass_noalloc(km_ctx *c, const float *X, int64_t rows, int32_t dims, const float *C, int32_t k,
+                                   double *totals, uint32_t *labels, float *best, void *stream) {
+    if (!c) return KM_EINVAL;
+    if (!X || !C || !totals || !labels || !best)
+        return fail(c, KM_EINVAL, "km_pass_noalloc: rows, centres, totals, labels and best must all be device pointers");
+    if (rows < 1 || dims < 1) return fail(c, KM_EINVAL, "expected a nonempty 2-D (rows, dims) array, got %lld x %d",
+                                          (long long)rows, dims);
+    if (k < 1) return fail(c, KM_EINVAL, "n_clusters must be a positive integer");
+    if (!c->scratch) return fail(c, KM_EDEVICE, "km_pass_noalloc: the scratch array's device address is unknown");
+    const int d = dims;
+    const int64_t kw = (int64_t)k * (d + 2);
+    hipStream_t s = (hipStream_t)stream;
+    HIPCHK(c, hipSetDevice(c->device));
+    const bool al = ((uintptr_t)X % 16) == 0;
+    ScratchCarve sc{c->scratch, 0, KM_SCRATCH_BYTES};
+    km_control *ctl = nullptr;
+    sc.take(&ctl, 1);
+    // the family km_pass would run, the wide-row path excepted
+    km_mfma_plan mp = km_plan_mfma(c->dev, rows, d, k);
+    if (!al) mp.ok = 0;
+    int fam;
+    if (mp.ok && d >= 16 && (int64_t)k * d >= 192) fam = FAM_MFMA_FUSED;
+    else if (km_plan_lowd(c->dev, rows, d, k, al).ok) fam = FAM_LOWD;
+    else fam = FAM_ROWS;
+    // the fused MFMA pass also accumulates [count, best] from its labels for the per-cluster best sums
+    const int64_t kw2 = (int64_t)k * 2;
+    km_accum_plan p2{};
+    size_t extra = 0;
+    if (fam == FAM_MFMA_FUSED) {
+        const size_t avail2 = KM_SCRATCH_BYTES / 8;
+        p2 = km_plan_accum_generic(rows, 0, k, na_max_blocks(avail2, kw2));
+        extra = na_reduce_bytes(p2.nrb, kw2) + ((size_t)kw2 * sizeof(double) + 255) / 256 * 256;
+        if (extra > avail2)
+            return fail(c, KM_EINVAL, "km_pass_noalloc: k = %d needs more than the %zu bytes of scratch", k,
+                        (size_t)KM_SCRATCH_BYTES);
+    }
+    const size_t avail = KM_SCRATCH_BYTES - sc.used - extra;
+    const int64_t maxb = na_max_blocks(avail, kw);
+    if (maxb < 1)
+        return fail(c, KM_EINVAL, "km_pass_noalloc: k * (dims + 2) = %lld entries need more than the %zu bytes of "
+                    "scratch (one block's partials and range sums); use km_pass", (long long)kw,
+                    (size_t)KM_SCRATCH_BYTES);
+    int nrb;
+    km_lowd_plan lp{};
+    km_accum_plan ap{};
+    if (fam == FAM_MFMA_FUSED) {
+        mp = km_plan_mfma(c->dev, rows, d, k, maxb);
+        nrb = mp.nrb;
+    } else if (fam == FAM_LOWD) {
+        lp = km_plan_lowd(c->dev, rows, d, k, al, maxb);
+        nrb = lp.nrb;
+    } else {
+        ap = km_plan_accum_generic(rows, d, k, maxb);
+        nrb = ap.nrb;
+    }
+    const int S = km_reduce_splits(nrb, kw);
+    float *psum = nullptr, *pcomp = nullptr;
+    double *red = nullptr;
+    if (!sc.take(&psum, (size_t)nrb * kw) || !sc.take(&pcomp, (size_t)nrb * kw) || !sc.take(&red, (size_t)S * kw))
+        return fail(c, KM_EINVAL, "km_pass_noalloc: the pass needs more than the %zu bytes of scratch",
+                    (size_t)KM_SCRATCH_BYTES);
+    hipLaunchKernelGGL(k_na_clear, dim3(1), dim3(256), 0, s, (uint32_t *)ctl, (int)(sizeof(km_control) / 4));
+    HIPCHK(c, hipGetLastError());
+    if (fam == FAM_MFMA_FUSED) {
+        HIPCHK(c, km_launch_mfma(mp, 1, X, rows, d, C, k, labels, best, psum, pcomp, 0, ctl, nullptr, s));
+    } else if (fam == FAM_LOWD) {
+        HIPCHK(c, km_launch_lowd(lp, X, rows, d, C, k, labels, best, psum, pcomp, 0, nullptr, s));
+    } else {
+        HIPCHK(c, km_launch_assign_rows(X, rows, d, C, k, labels, best, nullptr, s));
+        HIPCHK(c, km_launch_accum_generic(ap, X, rows, d, labels, best, k, psum, pcomp, 0, nullptr, s));
+    }
+    HIPCHK(c, km_launch_reduce_split(psum, pcomp, nrb, kw, S, red, nullptr, s));
+    HIPCHK(c, km_launch_finish(red, S, k, d, totals, nullptr, ctl, 0, 0.0, 0, nullptr, s));
+    if (fam == FAM_MFMA_FUSED) {
+        // per-cluster best sums: [count, best] accumulated from this pass's labels and best (as km_pass does)
+        const int S2 = km_reduce_splits(p2.nrb, kw2);
+        float *ps2 = nullptr, *pc2 = nullptr;
+        double *red2 = nullptr, *tot2 = nullptr;
+        if (!sc.take(&ps2, (size_t)p2.nrb * kw2) || !sc.take(&pc2, (size_t)p2.nrb * kw2) ||
+            !sc.take(&red2, (size_t)S2 * kw2) || !sc.take(&tot2, (size_t)kw2))
+            return fail(c, KM_EINVAL, "km_pass_noalloc: the pass needs more than the %zu bytes of scratch",
+                        (size_t)KM_SCRATCH_BYTES);
+        HIPCHK(c, km_launch_accum_generic(p2, nullptr, rows, 0, labels, best, k, ps2, pc2, 0, nullptr, s));
+        HIPCHK(c, km_launch_reduce_split(ps2, pc2, p2.nrb, kw2, S2, red2, nullptr, s));
+        HIPCHK(c, km_launch_finish(red2, S2, k, 0, tot2, nullptr, ctl, 0, 0.0, 0, nullptr, s));
+        hipLaunchKernelGGL(k_na_best_col, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, s, tot2, k, d + 2, totals);
+        HIPCHK(c, hipGetLastError());
+    }
+    c->last_path = family_path(fam);
     return KM_OK;
 }
 

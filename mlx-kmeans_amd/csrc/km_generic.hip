@@ -107,7 +107,7 @@ static int next_pow2(int v) {
 
 static constexpr size_t KM_ACC_LDS_BUDGET = 48 * 1024;
 
-km_accum_plan km_plan_accum_generic(int64_t n, int d, int k) {
+km_accum_plan km_plan_accum_generic(int64_t n, int d, int k, int64_t max_rb) {
     km_accum_plan pl{};
     const int w = d + 2;
     pl.wb = w < 2048 ? w : 2048;
@@ -124,6 +124,7 @@ km_accum_plan km_plan_accum_generic(int64_t n, int d, int k) {
     if (target_rb < 1) target_rb = 1;
     int64_t rbs = (n + target_rb - 1) / target_rb;
     if (rbs < 2048) rbs = 2048;
+    if (max_rb > 0 && (n + rbs - 1) / rbs > max_rb) rbs = (n + max_rb - 1) / max_rb;
     rbs = (rbs + 255) / 256 * 256;
     pl.rbs = rbs;
     pl.nrb = (int)((n + rbs - 1) / rbs);

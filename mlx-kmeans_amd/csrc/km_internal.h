@@ -76,7 +76,8 @@ struct km_accum_plan {
     int wb, nwb;     // columns per column-block, column-blocks
     size_t lds;      // dynamic LDS bytes
 };
-km_accum_plan km_plan_accum_generic(int64_t n, int d, int k);
+// max_rb > 0: at most that many row-blocks (longer blocks), so the partials fit a caller's budget
+km_accum_plan km_plan_accum_generic(int64_t n, int d, int k, int64_t max_rb = 0);
 hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int64_t n, int d,
                                    const uint32_t *labels, const float *best, int k, float *psum,
                                    float *pcomp, int rb0, const int32_t *stop, hipStream_t s);
@@ -115,7 +116,8 @@ struct km_mfma_plan {
     int waves;       // waves per block
     size_t lds;
 };
-km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k);
+// max_blocks > 0: at most that many workgroups (each takes more row blocks), so the partials fit a budget
+km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, int64_t max_blocks = 0);
 // want_best: every row's exact direct-form distance (labels/best outputs); without it, rows the screen settles
 // alone add an FMA-form distance to the pass inertia (their labels are exact either way).
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
@@ -131,7 +133,7 @@ struct km_lowd_plan {
     size_t lds;      // dynamic LDS bytes
     int lsh;         // the wave keeps 64 >> lsh tile columns; 1 << lsh lanes take turns on each
 };
-km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned);
+km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned, int64_t max_blocks = 0);
 hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int d, const float *C, int k,
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s);

@@ -441,7 +441,7 @@ static int lowd_rows_per_iter(int d) { return 64 * (d <= 8 ? 8 : 4); }
 // (20M rows: d = 4, k = 32 -21 %; d = 2, k = 48 -15 %) and not below (d = 4, k = 12 +5 %; d = 8, k = 8 +1 %).
 static bool lowd_screen(int k) { return k >= 24; }
 
-km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned) {
+km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned, int64_t max_blocks) {
     km_lowd_plan pl{};
     if (d < 1 || d > 16 || k < 1 || n < 1) return pl;
     if ((int64_t)k * (d + 2) > KM_LOWD_MAX_KW) return pl;
@@ -467,6 +467,7 @@ km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bo
     const int64_t units = (n + unit - 1) / unit;
     int64_t nrb = (int64_t)dev.cus * occ;
     if (nrb > units) nrb = units;
+    if (max_blocks > 0 && nrb > max_blocks) nrb = max_blocks;
     if (nrb < 1) nrb = 1;
     int64_t rbs = (n + nrb - 1) / nrb;
     rbs = (rbs + unit - 1) / unit * unit;

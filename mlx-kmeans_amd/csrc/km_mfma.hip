@@ -741,7 +741,7 @@ static const fused_entry *find_fused(int d, int k) {
     return nullptr;
 }
 
-km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k) {
+km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, int64_t max_blocks) {
     km_mfma_plan pl{};
     const fused_entry *fe = find_fused(d, k);
     if (!fe || n < 1) return pl;
@@ -770,6 +770,7 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k) {
     const int64_t unit = 64 * waves;
     const int64_t units = (n + unit - 1) / unit;
     int64_t nrb = units < slots ? units : slots;
+    if (max_blocks > 0 && nrb > max_blocks) nrb = max_blocks;
     if (nrb < 1) nrb = 1;
     pl.nrb = (int)nrb;
     pl.rbs = (units + nrb - 1) / nrb * unit;   // at most this many rows per block

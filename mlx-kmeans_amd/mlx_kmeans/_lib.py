@@ -41,6 +41,8 @@ SIGNATURES = [
     ("km_last_path", _c.c_int32, [_c.c_void_p]),
     ("km_last_fallback_rows", _c.c_int64, [_c.c_void_p]),
     ("km_version", _c.c_int32, []),
+    ("km_pass_noalloc", _c.c_int32, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int32, _c.c_void_p, _c.c_int32,
+                                     _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p]),
 ]
 
 _lib = None
