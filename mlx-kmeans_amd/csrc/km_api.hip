@@ -79,6 +79,8 @@ struct km_ctx {
     DBuf<uint16_t> cand;
     DBuf<uint32_t> hist, counts, base, perm, over, multi;
     DBuf<uint32_t> xmax;    // wide-row path: the largest |x|^2 over every slice (float bits)
+    DBuf<uint8_t> lstate;   // the fit loop's label of every row (one byte; each slice at lstate_off[i])
+    std::vector<int64_t> lstate_off;
     DBuf<float> Cb[2];      // centre buffers (k, d): pass p reads Cb[p & 1], writes Cb[(p + 1) & 1]
     DBuf<float> psum, pcomp;
     DBuf<double> tot;
@@ -230,6 +232,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->over.release();
     c->multi.release();
     c->xmax.release();
+    c->lstate.release();
     c->red.release();
     c->labels.release();
     c->best.release();
@@ -375,13 +378,16 @@ static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags
                        int presummed = 0) {
     const int d = c->d;
     const int64_t kw = (int64_t)k * (d + 2);
-    int S = presummed;
-    if (!presummed) {
-        S = km_reduce_splits(rb, kw);
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce_split(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, stop, c->stream); }));
-    }
     float *Cn = c->Cb[(pass + 1) & 1].p;
-    HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, S, k, d, c->tot.p, Cn, c->ctl, pass, tol, flags, stop, c->stream); }));
+    if (!presummed) {
+        const int S = km_reduce_splits(rb, kw);
+        HIPCHK(c, launch(c, KK_REDUCE, [&] {
+            return km_launch_reduce_finish(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, k, d, c->tot.p, Cn, c->ctl, pass,
+                                           tol, flags, stop, c->stream);
+        }));
+        return KM_OK;
+    }
+    HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, presummed, k, d, c->tot.p, Cn, c->ctl, pass, tol, flags, stop, c->stream); }));
     return KM_OK;
 }
 
@@ -473,7 +479,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
 // (float64 totals in c->tot; with KM_FIN_UPDATE in flags the new centres and the statistics). labels_d/best_d:
 // device arrays of n (or null) for the per-row results. gated: every kernel checks ctl->stop first.
 static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, float *best_d, bool gated, int pass,
-                    double tol, int flags) {
+                    double tol, int flags, int lmode = KM_LSTATE_NONE) {
     HIPCHK(c, c->Cb[(pass + 1) & 1].ensure((size_t)k * c->d));
     const float *Cin = c->Cb[pass & 1].p;
     km_mfma_plan mp;
@@ -505,14 +511,15 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             const Part &p = c->parts[i];
             uint32_t *lab = labels_d ? labels_d + row0 : nullptr;
             float *bst = best_d ? best_d + row0 : nullptr;
+            uint8_t *ls = lmode != KM_LSTATE_NONE ? c->lstate.p + c->lstate_off[i] : nullptr;
             HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
                 return km_launch_mfma(plans[i], want_best, p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p,
-                                      rb, c->ctl, stop, c->stream);
+                                      rb, c->ctl, ls, ls, lmode, stop, c->stream);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        return finish_pass(c, k, rb, pass, tol, flags, stop);
+        return finish_pass(c, k, rb, pass, tol, flags | (lmode == KM_LSTATE_DELTA ? KM_FIN_DELTA : 0), stop);
     }
 
     if (fam == FAM_LOWD) {
@@ -647,8 +654,10 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        HIPCHK(c, launch(c, KK_REDUCE, [&] { return km_launch_reduce_split(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, S2, c->red.p, nullptr, c->stream); }));
-        HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, S2, k, 0, c->tot2.p, nullptr, c->ctl, 0, 0.0, 0, nullptr, c->stream); }));
+        HIPCHK(c, launch(c, KK_REDUCE, [&] {
+            return km_launch_reduce_finish(c->psum.p, c->pcomp.p, rb, (int64_t)k * 2, S2, c->red.p, k, 0, c->tot2.p,
+                                           nullptr, c->ctl, 0, 0.0, 0, nullptr, c->stream);
+        }));
         cb2.resize((size_t)k * 2);
         HIPCHK(c, hipMemcpyAsync(cb2.data(), c->tot2.p, cb2.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
     }
@@ -734,9 +743,27 @@ static int relocate(km_ctx *c, int k, int mode, int path, int pass, int *n_empty
 }
 
 // Queues pass `pass` of a loop, gated on the control block.
-static int queue_iteration(km_ctx *c, int k, int mode, int path, int pass, double tol, int spherical) {
+static int queue_iteration(km_ctx *c, int k, int mode, int path, int pass, double tol, int spherical,
+                           int lmode = KM_LSTATE_NONE) {
     return run_pass(c, k, mode, path, nullptr, nullptr, true, pass, tol,
-                    KM_FIN_UPDATE | (spherical ? KM_FIN_SPHERICAL : 0));
+                    KM_FIN_UPDATE | (spherical ? KM_FIN_SPHERICAL : 0), lmode);
+}
+
+// The fit loop keeps every row's label between passes where the fused MFMA path runs, so that a pass accumulates
+// only the rows whose label changed. Sizes the label array (each slice's at a 64-row-aligned offset, 64 bytes of
+// padding after it). Returns whether the loop uses it.
+static int prepare_label_state(km_ctx *c, int k, bool *use) {
+    km_mfma_plan mp;
+    *use = choose_path(c, k, KM_PATH_AUTO, &mp) == FAM_MFMA_FUSED && k <= 256;
+    if (!*use) return KM_OK;
+    c->lstate_off.clear();
+    int64_t off = 0;
+    for (auto &p : c->parts) {
+        c->lstate_off.push_back(off);
+        off += (p.rows + 64 + 63) / 64 * 64;
+    }
+    HIPCHK(c, c->lstate.ensure((size_t)off));
+    return KM_OK;
 }
 
 extern "C" int32_t km_lloyd_step(km_ctx *c, const float *C, int32_t k, int32_t mode, int32_t path, float *C_out,
@@ -775,11 +802,18 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     if ((r = reset_control(c, tol))) return r;
     if (spherical) HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->Cb[0].p, k, c->d, c->stream); }));
     const int path = KM_PATH_AUTO;
+    bool use_ls = false;
+    if ((r = prepare_label_state(c, k, &use_ls))) return r;
+    // the pass that records every label (the first, and the first after a relocation); later passes accumulate
+    // only the rows whose label changed
+    int rec_pass = 0;
     int pass = 0, relocated = 0;
     while (pass < max_iter) {
         const int batch = std::min(KM_FIT_BATCH, max_iter - pass);
-        for (int i = 0; i < batch; i++)
-            if ((r = queue_iteration(c, k, mode, path, pass + i, tol, spherical))) return r;
+        for (int i = 0; i < batch; i++) {
+            const int lm = !use_ls ? KM_LSTATE_NONE : (pass + i == rec_pass ? KM_LSTATE_RECORD : KM_LSTATE_DELTA);
+            if ((r = queue_iteration(c, k, mode, path, pass + i, tol, spherical, lm))) return r;
+        }
         if ((r = read_control(c))) return r;
         pass = c->ctl_h->iter;
         if (c->ctl_h->need_reloc) {
@@ -787,6 +821,7 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
             const int q = c->ctl_h->iter - 1;   // the pass that left clusters empty
             if ((r = relocate(c, k, mode, path, q, &ne))) return r;
             relocated += ne;
+            rec_pass = q + 1;   // relocation moved rows and totals: the next pass starts the label state again
             if (spherical)
                 HIPCHK(c, launch(c, KK_NORMALISE, [&] { return km_launch_normalise(c->Cb[(q + 1) & 1].p, k, c->d, c->stream); }));
             c->ctl_h->need_reloc = 0;
@@ -971,15 +1006,15 @@ extern "C" int32_t km_pass_noalloc(km_ctx *c, const float *X, int64_t rows, int3
     hipLaunchKernelGGL(k_na_clear, dim3(1), dim3(256), 0, s, (uint32_t *)ctl, (int)(sizeof(km_control) / 4));
     HIPCHK(c, hipGetLastError());
     if (fam == FAM_MFMA_FUSED) {
-        HIPCHK(c, km_launch_mfma(mp, 1, X, rows, d, C, k, labels, best, psum, pcomp, 0, ctl, nullptr, s));
+        HIPCHK(c, km_launch_mfma(mp, 1, X, rows, d, C, k, labels, best, psum, pcomp, 0, ctl, nullptr, nullptr,
+                                 KM_LSTATE_NONE, nullptr, s));
     } else if (fam == FAM_LOWD) {
         HIPCHK(c, km_launch_lowd(lp, X, rows, d, C, k, labels, best, psum, pcomp, 0, nullptr, s));
     } else {
         HIPCHK(c, km_launch_assign_rows(X, rows, d, C, k, labels, best, nullptr, s));
         HIPCHK(c, km_launch_accum_generic(ap, X, rows, d, labels, best, k, psum, pcomp, 0, nullptr, s));
     }
-    HIPCHK(c, km_launch_reduce_split(psum, pcomp, nrb, kw, S, red, nullptr, s));
-    HIPCHK(c, km_launch_finish(red, S, k, d, totals, nullptr, ctl, 0, 0.0, 0, nullptr, s));
+    HIPCHK(c, km_launch_reduce_finish(psum, pcomp, nrb, kw, S, red, k, d, totals, nullptr, ctl, 0, 0.0, 0, nullptr, s));
     if (fam == FAM_MFMA_FUSED) {
         // per-cluster best sums: [count, best] accumulated from this pass's labels and best (as km_pass does)
         const int S2 = km_reduce_splits(p2.nrb, kw2);
@@ -990,8 +1025,7 @@ extern "C" int32_t km_pass_noalloc(km_ctx *c, const float *X, int64_t rows, int3
             return fail(c, KM_EINVAL, "km_pass_noalloc: the pass needs more than the %zu bytes of scratch",
                         (size_t)KM_SCRATCH_BYTES);
         HIPCHK(c, km_launch_accum_generic(p2, nullptr, rows, 0, labels, best, k, ps2, pc2, 0, nullptr, s));
-        HIPCHK(c, km_launch_reduce_split(ps2, pc2, p2.nrb, kw2, S2, red2, nullptr, s));
-        HIPCHK(c, km_launch_finish(red2, S2, k, 0, tot2, nullptr, ctl, 0, 0.0, 0, nullptr, s));
+        HIPCHK(c, km_launch_reduce_finish(ps2, pc2, p2.nrb, kw2, S2, red2, k, 0, tot2, nullptr, ctl, 0, 0.0, 0, nullptr, s));
         hipLaunchKernelGGL(k_na_best_col, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, s, tot2, k, d + 2, totals);
         HIPCHK(c, hipGetLastError());
     }

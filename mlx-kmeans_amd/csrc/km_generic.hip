@@ -236,11 +236,11 @@ int km_reduce_splits(int nrb, int64_t kw) {
     return s;
 }
 
-__global__ __launch_bounds__(1024) void k_reduce_split(const float *__restrict__ psum,
-                                                       const float *__restrict__ pcomp, int nrb, int64_t kw, int S,
-                                                       double *__restrict__ tmp, const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    __shared__ double part[16][64];
+// Block (x, y) of 1024 threads: entries 64 x .. 64 x + 63, range y of the S ranges of row-blocks. COHERENT: the range
+// sums are written with device-scope stores (through to the point of coherence, no L2-wide write-back).
+template <bool COHERENT>
+__device__ void reduce_split_body(const float *__restrict__ psum, const float *__restrict__ pcomp, int nrb, int64_t kw,
+                                  int S, double *__restrict__ tmp, double (*part)[64]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t e = (int64_t)blockIdx.x * 64 + lane;
     const int sp = blockIdx.y;
@@ -257,8 +257,17 @@ __global__ __launch_bounds__(1024) void k_reduce_split(const float *__restrict__
     if (wave == 0 && e < kw) {
         double t = part[0][lane];
         for (int w = 1; w < 16; w++) t += part[w][lane];
-        tmp[(int64_t)sp * kw + e] = t;
+        if (COHERENT) __hip_atomic_store(&tmp[(int64_t)sp * kw + e], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else tmp[(int64_t)sp * kw + e] = t;
     }
+}
+
+__global__ __launch_bounds__(1024) void k_reduce_split(const float *__restrict__ psum,
+                                                       const float *__restrict__ pcomp, int nrb, int64_t kw, int S,
+                                                       double *__restrict__ tmp, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    __shared__ double part[16][64];
+    reduce_split_body<false>(psum, pcomp, nrb, kw, S, tmp, part);
 }
 
 hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
@@ -338,22 +347,28 @@ __device__ void normalise_row(float *Cnext, int c, int d, int lane) {
         for (int j = lane; j < d; j += 64) row[j] = row[j] / nrm;
 }
 
-__global__ __launch_bounds__(1024) void k_finish1(const double *__restrict__ tmp, int S, int k, int d,
-                                                  double *__restrict__ tot, float *__restrict__ Cnext,
-                                                  km_control *__restrict__ ctl, int pass, double tol, int flags,
-                                                  const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    extern __shared__ double Ts[];   // the totals, k * (d + 2)
+// The single-block finish (1024 threads; Ts: k (d + 2) doubles of LDS): range sums -> totals, the update and the
+// pass statistics. COHERENT: the range sums are read with device-scope loads (written by other blocks of the same
+// launch).
+template <bool COHERENT>
+__device__ void finish1_body(const double *__restrict__ tmp, int S, int k, int d, double *__restrict__ tot,
+                             float *__restrict__ Cnext, km_control *__restrict__ ctl, int pass, double tol, int flags,
+                             double *Ts) {
     const int tid = threadIdx.x, W = d + 2;
     const int kw = k * W;
     for (int e = tid; e < kw; e += 1024) {
         double v[KM_FIN1_SPLITS];
 #pragma unroll
-        for (int sp = 0; sp < KM_FIN1_SPLITS; sp++) v[sp] = sp < S ? tmp[(int64_t)sp * kw + e] : 0.0;
+        for (int sp = 0; sp < KM_FIN1_SPLITS; sp++) {
+            double *src = const_cast<double *>(tmp) + (int64_t)sp * kw + e;
+            v[sp] = sp < S ? (COHERENT ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *src)
+                           : 0.0;
+        }
         double t = v[0];
 #pragma unroll
         for (int sp = 1; sp < KM_FIN1_SPLITS; sp++)
             if (sp < S) t += v[sp];
+        if ((flags & KM_FIN_DELTA) && e % W != 1) t = tot[e] + t;   // the previous totals plus their change
         Ts[e] = t;
         tot[e] = t;
     }
@@ -374,6 +389,43 @@ __global__ __launch_bounds__(1024) void k_finish1(const double *__restrict__ tmp
     pass_stats<1024>(Ts, k, d, Cnext, ctl, pass, tol);
 }
 
+__global__ __launch_bounds__(1024) void k_finish1(const double *__restrict__ tmp, int S, int k, int d,
+                                                  double *__restrict__ tot, float *__restrict__ Cnext,
+                                                  km_control *__restrict__ ctl, int pass, double tol, int flags,
+                                                  const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    extern __shared__ double Ts[];   // the totals, k * (d + 2)
+    finish1_body<false>(tmp, S, k, d, tot, Cnext, ctl, pass, tol, flags, Ts);
+}
+
+// k_reduce_split whose last block to finish runs the single-block finish: one launch per pass instead of two. Each
+// block writes its range sums through to the point of coherence and waits for those stores to complete before it
+// takes a ticket; the block that takes the last ticket reads them back with device-scope loads (across XCDs),
+// finishes, and resets the ticket for the next launch. No L2-wide write-back or invalidate is needed.
+__global__ __launch_bounds__(1024) void k_reduce_finish(const float *__restrict__ psum,
+                                                        const float *__restrict__ pcomp, int nrb, int64_t kw, int S,
+                                                        double *__restrict__ tmp, int k, int d,
+                                                        double *__restrict__ tot, float *__restrict__ Cnext,
+                                                        km_control *__restrict__ ctl, int pass, double tol, int flags,
+                                                        const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    __shared__ double part[16][64];
+    __shared__ int s_last;
+    extern __shared__ double Ts[];   // the totals, k * (d + 2) (used by the last block)
+    reduce_split_body<true>(psum, pcomp, nrb, kw, S, tmp, part);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned total = gridDim.x * gridDim.y;
+        const unsigned prev = __hip_atomic_fetch_add(&ctl->ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == total - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    finish1_body<true>(tmp, S, k, d, tot, Cnext, ctl, pass, tol, flags, Ts);
+    if (threadIdx.x == 0) __hip_atomic_store(&ctl->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __global__ __launch_bounds__(256) void k_finish(const double *__restrict__ tmp, int S, int k, int d,
                                                 double *__restrict__ tot, float *__restrict__ Cnext, int flags,
                                                 const int32_t *__restrict__ stop) {
@@ -383,13 +435,17 @@ __global__ __launch_bounds__(256) void k_finish(const double *__restrict__ tmp, 
     // entry j of this cluster = its S range sums added in ascending order by thread j (and every thread adds the
     // count's own, the same way, to divide by it)
     const double *src = tmp + (int64_t)c * W;
+    const bool delta = (flags & KM_FIN_DELTA) != 0;
     double cntd = 0.0;
     for (int sp = 0; sp < S; sp++) cntd += src[(int64_t)sp * kw];
+    if (delta) cntd = tot[(int64_t)c * W] + cntd;
     const long long cnt = llrint(cntd);
     const bool update = (flags & KM_FIN_UPDATE) != 0;
+    __syncthreads();   // every thread has read the previous count before thread 0 overwrites it
     for (int j = threadIdx.x; j < W; j += 256) {
         double v = 0.0;
         for (int sp = 0; sp < S; sp++) v += src[(int64_t)sp * kw + j];
+        if (delta && j != 1) v = tot[(int64_t)c * W + j] + v;   // the previous totals plus their change
         tot[(int64_t)c * W + j] = v;
         if (update && j >= 2 && cnt > 0) Cnext[(int64_t)c * d + (j - 2)] = (float)(v / (double)cnt);
     }
@@ -404,6 +460,19 @@ __global__ __launch_bounds__(256) void k_stats(const double *__restrict__ tot, i
                                                double tol, const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
     pass_stats<256>(tot, k, d, Cnext, ctl, pass, tol);
+}
+
+hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
+                                   int k, int d, double *tot, float *Cnext, km_control *ctl, int pass, double tol,
+                                   int flags, const int32_t *stop, hipStream_t s) {
+    if (kw <= KM_FIN1_MAX && S <= KM_FIN1_SPLITS) {
+        hipLaunchKernelGGL(k_reduce_finish, dim3((unsigned)((kw + 63) / 64), S), dim3(1024), (size_t)kw * sizeof(double),
+                           s, psum, pcomp, nrb, kw, S, tmp, k, d, tot, Cnext, ctl, pass, tol, flags, stop);
+        return hipGetLastError();
+    }
+    hipError_t e = km_launch_reduce_split(psum, pcomp, nrb, kw, S, tmp, stop, s);
+    if (e != hipSuccess) return e;
+    return km_launch_finish(tmp, S, k, d, tot, Cnext, ctl, pass, tol, flags, stop, s);
 }
 
 hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,

@@ -37,6 +37,8 @@ struct km_control {
     double prev;         // inertia of the pass before it
     double tol;
     uint64_t fallback_rows;  // rows the MFMA screen left to a full rescoring, summed over passes
+    uint32_t ticket;         // blocks of the running reduce that have written their range sums (reset by the last)
+    uint32_t pad_;
 };
 
 // What the planners need to know of the device a context runs on (read once, in km_create).
@@ -91,9 +93,16 @@ hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb
 // stopping rule into ctl (pass `pass`, tolerance tol); KM_FIN_SPHERICAL renormalises the new centres.
 #define KM_FIN_UPDATE 1
 #define KM_FIN_SPHERICAL 2
+#define KM_FIN_DELTA 4    // the range sums are the change since the previous pass: added to tot (the inertia
+                          // column, column 1, is the pass's own)
 hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,
                             int pass, double tol, int flags, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_normalise(float *C, int k, int d, hipStream_t s);
+// The reduce and the finish in one launch where the single-block finish serves the shape (the reduce's last block
+// finishes), else the two launches.
+hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
+                                   int k, int d, double *tot, float *Cnext, km_control *ctl, int pass, double tol,
+                                   int flags, const int32_t *stop, hipStream_t s);
 
 // Greedy k-means++ on a device-resident sample of the rows, held transposed as ST (d x m) (km_seed.hip).
 // km_pp_trials(k) candidates per round (at most KM_PP_MAX_TRIALS); ws: km_pp_workspace(m, k) bytes; seeds_h:
@@ -120,9 +129,16 @@ struct km_mfma_plan {
 km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, int64_t max_blocks = 0);
 // want_best: every row's exact direct-form distance (labels/best outputs); without it, rows the screen settles
 // alone add an FMA-form distance to the pass inertia (their labels are exact either way).
+// Label state of a fit (lmode, without want_best): 0 none; KM_LSTATE_RECORD every row's label goes to lout (one
+// byte per row, the pass accumulates every row); KM_LSTATE_DELTA the pass reads the previous labels from lprev
+// (buffer padded by 64 bytes), accumulates only the rows whose label changed (+1, +x to the new cluster; -1, -x
+// to the old), so its partials hold the change of the totals, and writes the changed labels to lout.
+#define KM_LSTATE_NONE 0
+#define KM_LSTATE_RECORD 1
+#define KM_LSTATE_DELTA 2
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
-                          const int32_t *stop, hipStream_t s);
+                          const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s);
 
 // Fused single-read pass for dims <= 16: exact rows loop + deterministic accumulation into per-block partials.
 struct km_lowd_plan {

@@ -137,6 +137,24 @@ __device__ __forceinline__ void screen_tile(const bf16x8 (&B)[Geo<D, KP>::DS], c
     }
 }
 
+// screen_tile with the centre operand's dims K-steps from LDS (Alds[(t DS + s) 64 + lane], shared by the
+// workgroup's waves) and its |c|^2 K-step (Acsq) in registers
+template <int D, int KP>
+__device__ __forceinline__ void screen_tile_lds(const bf16x8 (&B)[Geo<D, KP>::DS], const bf16x8 *Alds, int lane,
+                                                const bf16x8 (&Acsq)[Geo<D, KP>::KT], const bf16x8 &Bone,
+                                                f32x16 (&a)[Geo<D, KP>::KT]) {
+    using G = Geo<D, KP>;
+    const f32x16 zero = {};
+#pragma unroll
+    for (int t = 0; t < G::KT; t++) {
+        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Alds[(t * G::DS) * 64 + lane], B[0], zero, 0, 0, 0);
+#pragma unroll
+        for (int s = 1; s < G::DS; s++)
+            a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Alds[(t * G::DS + s) * 64 + lane], B[s], a[t], 0, 0, 0);
+        a[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Acsq[t], Bone, a[t], 0, 0, 0);
+    }
+}
+
 template <int D, int KP>
 __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], float &m1, float &m2) {
     using G = Geo<D, KP>;
@@ -287,23 +305,36 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
     return *reinterpret_cast<const float *>(buf + row * (D * 4) + (((dim >> 2) ^ swz<D>(row)) * 16) + (dim & 3) * 4);
 }
 
-template <int D, int KP, int WAVES, bool ACCUM, bool BEST>
-__global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
+// (64-dim blocks hold 32 KB of rows per wave in LDS, so they run one wave per SIMD: the whole register file.)
+//
+// Label state across the passes of a fit (LM): 0 none; 1 every row's label is recorded in lout (one byte per row)
+// and the pass accumulates every row; 2 the pass reads the previous pass's labels (lprev, brought into LDS with
+// the block's rows) and accumulates only the rows whose label changed: +x and +1 for the new cluster, -x and -1
+// for the old one (a signed one-hot), so the partials are the change of the totals since the previous pass; a
+// 64-row block with no changed row skips the accumulation. The inertia is every row's, in every mode.
+template <int D, int KP, int WAVES, bool ACCUM, bool BEST, int LM>
+__global__ __launch_bounds__(64 * WAVES, D >= 64 ? 1 : 2) void k_fused_mfma(
     const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k,
     uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
-    int rb0, km_control *__restrict__ ctl, const int32_t *__restrict__ stop) {
+    int rb0, km_control *__restrict__ ctl, const uint8_t *__restrict__ lprev, uint8_t *__restrict__ lout,
+    const int32_t *__restrict__ stop) {
     using G = Geo<D, KP>;
     using L = Lay<D>;
     constexpr int DH = G::DH, DS = G::DS, KT = G::KT, CS = G::CS, W = D + 2;
     constexpr int NT = (D + 31) / 32;                 // 32-dim tiles of the accumulation
     constexpr int FOLD = (KP * 32 * NT + 2 * KP) * 4; // bytes of the end-of-block fold per wave
     // per wave: two block buffers, 64 uint16 labels and KP uint32 counts during the loop, the fold after it
-    constexpr int LOOPB = 2 * L::BUF + 128 + 4 * KP;
+    constexpr int LB = L::BUF + 64;                   // a block buffer: the rows, then their 64 previous labels
+    constexpr int LOOPB = 2 * LB + 256 + 4 * KP;     // + 64 uint16 labels (and 64 old labels)
+    constexpr int LX = LM == 2 ? 1 : 0;               // loads per block beyond the rows' (the labels)
     // one-hot bytes in the block buffer once its rows are in registers: KP rows of OHS bytes (64 rows + 8 bytes
     // of padding, so the 32 lanes of a half-wave reading 8 bytes each start on distinct even banks)
     constexpr int OHS = 72, OHB_BYTES = KP * OHS;
     constexpr bool OHB = NT == 1 && OHB_BYTES <= L::BUF;
     constexpr int WBYTES = (LOOPB > FOLD + 4 * KP) ? LOOPB : FOLD + 4 * KP;
+    constexpr int ABYTES = KT * DS * 64 * 16;         // the screen's centre operand, dims K-steps (per workgroup)
+    // each float32 accumulator run covers at most FOLDB blocks (64 FOLDB rows) before it is added into sfold
+    constexpr int FOLDB = 16;
     // window constants
     constexpr int NACC = G::DP + 2;
     constexpr float BETA = (float)((2.0 * (0x1p-8 + 0x1p-8 + 0x1p-16) + 2.04 * km_gamma(NACC)) * (1.0 + 0x1p-20));
@@ -323,9 +354,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 
     extern __shared__ float lds[];
     float *Cl = lds;                                  // KP x CS float32 centres
+    bf16x8 *Alds = reinterpret_cast<bf16x8 *>(lds + KP * CS);   // KT x DS x 64 lanes of bf16(-2c)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    char *wbase = reinterpret_cast<char *>(lds + KP * CS) + wave * WBYTES;
-    uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * L::BUF);   // labels of the block (0x4000: no row)
+    char *wbase = reinterpret_cast<char *>(lds + KP * CS) + ABYTES + wave * WBYTES;
+    uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * LB);       // labels of the block (0x4000: no row)
     uint32_t *CNT = reinterpret_cast<uint32_t *>(wbase + WBYTES - 4 * KP);   // rows per centre (this wave)
 
     // blocks of 64 WAVES rows go round-robin to the workgroups (at any time the whole grid streams one window of
@@ -335,6 +367,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     const uint32_t voff0 = issue_voff<D>(lane, 0), voff1 = issue_voff<D>(lane, 1);
     if (r0 + 64 <= r_end) issue_block_inner_all<D>(X + r0 * D, voff0, voff1, wbase);
     else if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, wbase);
+    if (LM == 2 && r0 < r_end && lane < 4) lds_dma16(lprev + r0 + 16 * lane, (lds_vptr)(wbase + L::BUF));
 
     for (int e = threadIdx.x; e < KP * CS; e += 64 * WAVES) {
         const int c = e / CS, j = e % CS;
@@ -348,7 +381,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     // candidate and finite so packed keys stay ordered) as two bf16 pieces against a B operand of ones, so
     // |c|^2 - 2 x.c comes out of the matrix cores directly. The window needs max |c| (rounded up) and max |c|^2
     // over the real centres.
-    bf16x8 Aop[KT][G::AK];
+    bf16x8 Acsq[KT];
     float cn_l = 0.0f, cs_l = 0.0f;
 #pragma unroll
     for (int t = 0; t < KT; t++) {
@@ -365,17 +398,22 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
             cn_l = fmaxf(cn_l, (float)(sqrt(sq) * (1.0 + 1e-6)));
             cs_l = fmaxf(cs_l, sf);
         }
+        if (wave == 0) {
 #pragma unroll
-        for (int st = 0; st < DS; st++)
+            for (int st = 0; st < DS; st++) {
+                bf16x8 av;
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const int j = h * DH + 8 * st + q;
-                const float v = (real && j < D) ? -2.0f * Cl[cA * CS + j] : 0.0f;
-                Aop[t][st][q] = (__bf16)v;
+                for (int q = 0; q < 8; q++) {
+                    const int j = h * DH + 8 * st + q;
+                    const float v = (real && j < D) ? -2.0f * Cl[cA * CS + j] : 0.0f;
+                    av[q] = (__bf16)v;
+                }
+                Alds[(t * DS + st) * 64 + lane] = av;
             }
+        }
         const float hi = (float)(__bf16)sf;
 #pragma unroll
-        for (int q = 0; q < 8; q++) Aop[t][DS][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
+        for (int q = 0; q < 8; q++) Acsq[t][q] = (__bf16)((h == 0 && q < 2) ? (q == 0 ? hi : sf - hi) : 0.0f);
     }
     for (int off = 32; off > 0; off >>= 1) {
         cn_l = fmaxf(cn_l, __shfl_xor(cn_l, off));
@@ -386,26 +424,32 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 #pragma unroll
     for (int q = 0; q < 8; q++) Bone[q] = (__bf16)((h == 0 && q < 2) ? 1.0f : 0.0f);
 
+    __syncthreads();   // Alds written by wave 0
     float ine_s = 0.0f, ine_c = 0.0f;   // Kahan inertia of this lane's rows
     uint32_t fallback = 0;
-    f32x16 sacc[KT][NT];
+    f32x16 sacc[KT][NT], sfold[KT][NT];
 #pragma unroll
     for (int t = 0; t < KT; t++)
 #pragma unroll
-        for (int u = 0; u < NT; u++) sacc[t][u] = f32x16{};
+        for (int u = 0; u < NT; u++) {
+            sacc[t][u] = f32x16{};
+            sfold[t][u] = f32x16{};
+        }
+    int nblk = 0;
     for (int c = lane; c < KP; c += 64) CNT[c] = 0u;
     const uint32_t ones = 0x00010001u, c3f80 = 0x3f803f80u, cneg = 0xc080c080u;
 
     // the two block buffers alternate by offset (pointer arithmetic keeps the LDS address space visible)
     int cur = 0;
-    for (; r0 < r_end; r0 += step, cur ^= L::BUF) {
+    for (; r0 < r_end; r0 += step, cur ^= LB) {
         const char *buf = wbase + cur;
         // ---- prefetch the next block into the other buffer, then wait for this one
         const int64_t r1 = r0 + step;
         if (r1 < r_end) {
-            if (r1 + 64 <= r_end) issue_block_inner_all<D>(X + r1 * D, voff0, voff1, wbase + (cur ^ L::BUF));
-            else issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ L::BUF));
-            vm_wait<L::NC>();
+            if (r1 + 64 <= r_end) issue_block_inner_all<D>(X + r1 * D, voff0, voff1, wbase + (cur ^ LB));
+            else issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ LB));
+            if (LM == 2 && lane < 4) lds_dma16(lprev + r1 + 16 * lane, (lds_vptr)(wbase + (cur ^ LB) + L::BUF));
+            vm_wait<L::NC + LX>();
         } else {
             vm_wait<0>();
         }
@@ -420,14 +464,14 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
             bf16x8 B[DS];
             sa = make_b<D, KP>(xa, B);
             f32x16 a[KT];
-            screen_tile<D, KP>(B, Aop, Bone, a);
+            screen_tile_lds<D, KP>(B, Alds, lane, Acsq, Bone, a);
             min2_keys<D, KP>(a, m1a, m2a);
         }
         {
             bf16x8 B[DS];
             sb = make_b<D, KP>(xb, B);
             f32x16 a[KT];
-            screen_tile<D, KP>(B, Aop, Bone, a);
+            screen_tile_lds<D, KP>(B, Alds, lane, Acsq, Bone, a);
             min2_keys<D, KP>(a, m1b, m2b);
         }
         // ---- the owned row's two halves
@@ -536,9 +580,13 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
             own_halves((pa[0] + pa[1]) + (pa[2] + pa[3]), (pb[0] + pb[1]) + (pb[2] + pb[3]), s0h, s1h);
             if (unique) bst = s0h + s1h;
         }
+        // the previous pass's label of the owned row (LM 2), and whether the row changed cluster
+        const uint32_t prv = (LM == 2 && valid) ? (uint32_t)reinterpret_cast<const uint8_t *>(buf + L::BUF)[lane] : bl;
+        const bool moved = LM == 2 ? (valid && prv != bl) : valid;
         if (valid) {
             if (labels) labels[row] = bl;
             if (BEST && best) best[row] = bst;
+            if (LM == 1 || (LM == 2 && moved)) lout[row] = (uint8_t)bl;
         }
         if (ACCUM) {
             // ---- accumulation on the matrix cores: sums (centres x dims) += onehot^T (centres x rows) x rows
@@ -548,7 +596,11 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                 ine_c = (tt - ine_s) - y;
                 ine_s = tt;
             }
-            if (valid) atomicAdd(&CNT[bl], 1u);   // integer adds: the order does not matter
+            if (LM != 2 || __ballot(moved)) {
+            if (moved) {
+                atomicAdd(&CNT[bl], 1u);   // integer adds: the order does not matter
+                if (LM == 2) atomicAdd(&CNT[prv], 0xffffffffu);   // -1: the row left its old cluster
+            }
             if constexpr (OHB) {
                 // The block's rows in the accumulation's layout (lane = one dim, eight rows per K-step) go to
                 // registers first; then the block buffer holds the one-hot bytes: byte [c][r] = 0x40, the high
@@ -564,7 +616,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 #pragma unroll
                 for (int i = lane; i < OHB_BYTES / 16; i += 64) reinterpret_cast<uint4 *>(ohb)[i] = uint4{0u, 0u, 0u, 0u};
                 wave_sync();
-                if (valid) ohb[bl * OHS + lane] = (char)0x40;
+                if (moved) {
+                    ohb[bl * OHS + lane] = (char)0x40;
+                    if (LM == 2) ohb[prv * OHS + lane] = (char)0xc0;   // -2.0: the row leaves its old cluster
+                }
                 wave_sync();
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++) {
@@ -588,13 +643,22 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                     }
                 }
             } else {
-            L16[lane] = valid ? (uint16_t)bl : (uint16_t)0x4000u;
+            L16[lane] = moved ? (uint16_t)bl : (uint16_t)0x4000u;
+            if (LM == 2) L16[64 + lane] = moved ? (uint16_t)prv : (uint16_t)0x4000u;
             wave_sync();
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 const int rbase = 16 * ks + 8 * h;           // this lane's 8 rows of the K-step
                 const uint4 lp = *reinterpret_cast<const uint4 *>(L16 + rbase);   // 8 uint16 labels
                 const uint32_t lab2[4] = {lp.x, lp.y, lp.z, lp.w};
+                uint32_t old2[4] = {0u, 0u, 0u, 0u};
+                if (LM == 2) {
+                    const uint4 lq = *reinterpret_cast<const uint4 *>(L16 + 64 + rbase);   // their old labels
+                    old2[0] = lq.x;
+                    old2[1] = lq.y;
+                    old2[2] = lq.z;
+                    old2[3] = lq.w;
+                }
                 bf16x8 OH[KT];
 #pragma unroll
                 for (int t = 0; t < KT; t++) {
@@ -606,6 +670,12 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                         uint32_t y, oh;
                         asm("v_pk_min_u16 %0, %1, %2" : "=v"(y) : "v"(lab2[p] ^ mm), "v"(ones));
                         asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(oh) : "v"(y), "v"(cneg), "v"(c3f80));
+                        if (LM == 2) {   // -1 (0xbf80) where the row's old label matches; a moved row matches one
+                            uint32_t y2, oh2;
+                            asm("v_pk_min_u16 %0, %1, %2" : "=v"(y2) : "v"(old2[p] ^ mm), "v"(ones));
+                            asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(oh2) : "v"(y2), "v"(cneg), "v"(c3f80));
+                            oh |= oh2 | ((oh2 & 0x00800080u) << 8);   // 0x3f80 -> 0xbf80 (bit 7 marks a match)
+                        }
                         o[p] = oh;
                     }
                     OH[t] = *reinterpret_cast<bf16x8 *>(o);
@@ -627,12 +697,27 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
                 }
             }
             }
+            }   // a block with no changed row (LM 2) skips the accumulation
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (++nblk == FOLDB) {   // bound the float32 run: add it into sfold and start again
+                nblk = 0;
+#pragma unroll
+                for (int t = 0; t < KT; t++)
+#pragma unroll
+                    for (int u = 0; u < NT; u++) {
+                        sfold[t][u] += sacc[t][u];
+                        sacc[t][u] = f32x16{};
+                    }
+            }
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int t = 0; t < KT; t++)
+#pragma unroll
+        for (int u = 0; u < NT; u++) sacc[t][u] += sfold[t][u];
 
     if (fallback) atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)fallback);
     if (!ACCUM) return;
@@ -672,7 +757,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
     const int64_t kw = (int64_t)k * W;
     float *ps = psum + (int64_t)(rb0 + blockIdx.x) * kw;
     float *pc = pcomp + (int64_t)(rb0 + blockIdx.x) * kw;
-    const char *base = reinterpret_cast<const char *>(lds + KP * CS);
+    const char *base = reinterpret_cast<const char *>(lds + KP * CS) + ABYTES;   // the first wave's region
     for (int e = threadIdx.x; e < k * W; e += 64 * WAVES) {
         const int c = e / W, col = e % W;
         float s = 0.0f, cc = 0.0f;
@@ -680,7 +765,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
             uint32_t tot = 0;
             for (int w = 0; w < WAVES; w++)
                 tot += reinterpret_cast<const uint32_t *>(base + w * WBYTES + WBYTES - 4 * KP)[c];
-            s = (float)tot;
+            s = (float)(int32_t)tot;   // a change of the count (LM 2) may be negative
         } else if (col == 1) {
             if (c == 0) {
                 for (int w = 0; w < WAVES; w++) {
@@ -708,17 +793,21 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_fused_mfma(
 // ------------------------------------------------------------------ planning and launch
 
 typedef void (*fused_fn)(const float *, int64_t, const float *, int, uint32_t *, float *, float *, float *,
-                         int, km_control *, const int32_t *);
+                         int, km_control *, const uint8_t *, uint8_t *, const int32_t *);
 
 // One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
+// Per block size: the pass without label state, with the rows' exact distances ("b": labels and best outputs),
+// recording the labels ("r"), and accumulating only the rows whose label changed ("i").
 struct fused_entry {
     int d, kp;
-    fused_fn acc4, acc4b, acc2, acc2b;   // accumulating; "b": also the rows' exact distances (labels, best)
+    fused_fn acc4, acc4b, acc4r, acc4i, acc2, acc2b, acc2r, acc2i;
 };
 
 #define KM_FUSED(DD, KK)                                                                                     \
-    {DD, KK, k_fused_mfma<DD, KK, 4, true, false>, k_fused_mfma<DD, KK, 4, true, true>,                    \
-     k_fused_mfma<DD, KK, 2, true, false>, k_fused_mfma<DD, KK, 2, true, true>}
+    {DD, KK, k_fused_mfma<DD, KK, 4, true, false, 0>, k_fused_mfma<DD, KK, 4, true, true, 0>,              \
+     k_fused_mfma<DD, KK, 4, true, false, 1>, k_fused_mfma<DD, KK, 4, true, false, 2>,                     \
+     k_fused_mfma<DD, KK, 2, true, false, 0>, k_fused_mfma<DD, KK, 2, true, true, 0>,                      \
+     k_fused_mfma<DD, KK, 2, true, false, 1>, k_fused_mfma<DD, KK, 2, true, false, 2>}
 
 static fused_entry g_fused[] = {
     KM_FUSED(16, 32), KM_FUSED(16, 64),
@@ -727,11 +816,13 @@ static fused_entry g_fused[] = {
 };
 #undef KM_FUSED
 
-// mirrors the kernel's layout: centres, then per wave max(two block buffers + labels + counts, fold + counts)
+// mirrors the kernel's layout: centres, the screen operand, then per wave max(two block buffers with their labels
+// + label staging + counts, fold + counts)
 static size_t lds_for(int d, int kp, int waves) {
-    const size_t loop = 2 * (size_t)(64 * d * 4) + 128 + 4 * (size_t)kp;
+    const size_t loop = 2 * ((size_t)(64 * d * 4) + 64) + 256 + 4 * (size_t)kp;
     const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float) + 4 * (size_t)kp;
-    return (size_t)kp * (d + 1) * sizeof(float) + waves * (loop > fold ? loop : fold);
+    const size_t abytes = (size_t)(kp / 32) * ((d + 15) / 16) * 64 * 16;
+    return (size_t)kp * (d + 1) * sizeof(float) + abytes + waves * (loop > fold ? loop : fold);
 }
 
 static const fused_entry *find_fused(int d, int k) {
@@ -754,9 +845,10 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
     }
     fused_fn fn = waves == 4 ? fe->acc4 : fe->acc2;
     if (lds > 65536) {
-        (void)hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        (void)hipFuncSetAttribute((const void *)(waves == 4 ? fe->acc4b : fe->acc2b),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const fused_fn all[4] = {fn, waves == 4 ? fe->acc4b : fe->acc2b, waves == 4 ? fe->acc4r : fe->acc2r,
+                                 waves == 4 ? fe->acc4i : fe->acc2i};
+        for (fused_fn f : all)
+            (void)hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)fn, 64 * waves, lds) != hipSuccess || occ < 1)
@@ -779,11 +871,16 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
 
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
-                          const int32_t *stop, hipStream_t s) {
+                          const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s) {
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
-    fused_fn fn = pl.waves == 4 ? (want_best ? fe->acc4b : fe->acc4) : (want_best ? fe->acc2b : fe->acc2);
+    if (lmode != 0 && (want_best || !lout || (lmode == 2 && !lprev))) return hipErrorInvalidValue;
+    const bool w4 = pl.waves == 4;
+    fused_fn fn = want_best ? (w4 ? fe->acc4b : fe->acc2b)
+                  : lmode == 1 ? (w4 ? fe->acc4r : fe->acc2r)
+                  : lmode == 2 ? (w4 ? fe->acc4i : fe->acc2i)
+                               : (w4 ? fe->acc4 : fe->acc2);
     hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, labels, best, psum,
-                       pcomp, rb0, ctl, stop);
+                       pcomp, rb0, ctl, lprev, lout, stop);
     return hipGetLastError();
 }

@@ -444,3 +444,48 @@ def test_embed_workload_full_size(lib):
     tot2, labels2, _ = ctx.run_pass(C0, labels=True)
     assert np.array_equal(tot, tot2) and np.array_equal(labels, labels2)
     ctx.close()
+
+
+@pytest.mark.parametrize("d,k,parts", [(32, 64, 1), (16, 40, 2), (64, 32, 1), (32, 20, 3), (16, 64, 1)])
+def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts):
+    """The fit loop accumulates, after its first pass, only the rows whose label changed (into the new cluster, out of
+    the old one) and adds that to the previous pass's totals. The same number of Lloyd steps run one at a time with
+    a full accumulation each (km_lloyd_step) must reach the same centres (within 1e-6 of the RMS) and inertia
+    (within 1e-6), with the same iteration count under a tolerance; reruns of the loop are bit-identical. The data
+    keep rows moving between clusters for several passes (overlapping blobs, starting centres drawn from one
+    corner)."""
+    rng = np.random.default_rng(900 + d + k + parts)
+    n = 90_011
+    cen = rng.uniform(-3, 3, size=(k, d)).astype(np.float32)
+    X = (cen[rng.integers(0, k, n)] + 1.3 * rng.standard_normal((n, d))).astype(np.float32)
+    order = np.argsort(X[:, 0])
+    C0 = X[order[rng.choice(n // 3, k, replace=False)]].copy()
+    cuts = np.linspace(0, n, parts + 1).astype(int)
+    slices = [X[cuts[i]:cuts[i + 1]] for i in range(parts)]
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(slices)
+    steps = 12
+    say(f"[gpu] change accumulation d={d} k={k} parts={parts}")
+    C_fit, in_fit, it_fit, _ = ctx.fit(C0, steps, -1.0)
+    assert it_fit == steps
+    C = C0
+    moved = []
+    prev_lab = None
+    for s in range(steps):
+        _, lab, _ = ctx.run_pass(C, labels=True)
+        if prev_lab is not None:
+            moved.append(int((lab != prev_lab).sum()))
+        prev_lab = lab
+        C, inertia, _ = ctx.lloyd_step(C)
+    say(f"[gpu]   rows changing cluster per pass: {moved}")
+    assert sum(moved[:3]) > 0, "the data should move rows between clusters"
+    assert float(np.max(np.abs(C_fit.astype(np.float64) - C.astype(np.float64)))) / scale <= 1e-6
+    assert abs(in_fit - inertia) <= 1e-6 * inertia
+    C2, in2, _, _ = ctx.fit(C0, steps, -1.0)
+    assert np.array_equal(C2, C_fit) and in2 == in_fit
+    ref_C, _, ref_it, _ = __import__("oracle").fit_from(X, C0, max_iter=40, tol=1e-3)
+    C3, _, it3, _ = ctx.fit(C0, 40, 1e-3)
+    assert it3 == ref_it
+    assert float(np.max(np.abs(C3.astype(np.float64) - ref_C))) / scale <= 1e-5
+    ctx.close()
