@@ -53,9 +53,20 @@ def profile_summary(name):
     return None
 
 
+def cpu_threads():
+    """-> (threads used, description): the host CPUs this process may run on, capped at OMP_NUM_THREADS (the
+    share of a shared host's cores allotted to one GPU's jobs, 16 on the MI355X machines this runs on)."""
+    host = os.cpu_count() or 1
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or allowed
+    used = max(1, min(allowed, cap))
+    return used, (f"{used} threads: the host has {host} CPUs, this process may use {allowed}, and "
+                  f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')} is its share of a shared host")
+
+
 def cpu_baseline(X, C, budget_s=12.0):
     import oracle
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores, why = cpu_threads()
     n = len(X)
     rows = min(n, 2_000_000)
     sample = X[:rows]
@@ -70,8 +81,33 @@ def cpu_baseline(X, C, budget_s=12.0):
             break
     per_pass_ms = float(np.median(times)) * 1e3 * (n / rows)
     return {"value": round(per_pass_ms, 3), "unit": "ms/pass", "cores": cores, "kind": "port",
+            "host_cpus": os.cpu_count(), "threads_note": why,
             "sample": f"first {rows:,} of {n:,} rows, {len(times)} passes, median scaled by {n / rows:g}; "
                       f"kmeans.mm CPU backend restated (oracle/kmeans_oracle.c orc_cpu_pass)"}
+
+
+def cpu_baseline_numpy(X, C, budget_s=8.0):
+    """The second CPU baseline: kmeans_simple.py:45-78 restated in numpy (expanded-form distances through the
+    BLAS, argmin, scatter-add, float64 host totals), on a row sample scaled to the full workload."""
+    import oracle
+    cores, why = cpu_threads()
+    n = len(X)
+    rows = min(n, 1_000_000)
+    sample = X[:rows]
+    oracle.kmeans_simple_pass(sample[: min(rows, 20_000)], C)    # warm
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle.kmeans_simple_pass(sample, C)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > budget_s or len(times) >= 10:
+            break
+    per_pass_ms = float(np.median(times)) * 1e3 * (n / rows)
+    return {"value": round(per_pass_ms, 3), "unit": "ms/pass", "cores": cores, "kind": "port",
+            "host_cpus": os.cpu_count(), "threads_note": "BLAS " + why,
+            "sample": f"first {rows:,} of {n:,} rows, {len(times)} passes, median scaled by {n / rows:g}; "
+                      f"kmeans_simple.py restated in numpy (oracle.kmeans_simple_pass)"}
 
 
 def seed_probe(workload):
@@ -112,7 +148,15 @@ def main():
                     help="only time k-means++ seeding of the workload (GPU, and the host float64 version)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB with torch (a plain copy kernel of known size, for counter calibration)")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="only measure the HBM streaming-read rate (the library's probe kernel over 4 GiB)")
     a = ap.parse_args()
+    if a.stream_probe:
+        from mlx_kmeans import _lib
+        ctx = _lib.Context(0)
+        print(json.dumps({"stream_read_gbs": round(ctx.stream_probe(4 << 30, 20), 1), "bytes": 4 << 30}), flush=True)
+        ctx.close()
+        return
     if a.copy_probe:
         import torch
         x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
@@ -166,7 +210,11 @@ def main():
     ctx.profile(True)
     ctx.fit(C0, a.steps, -1.0, mode=mode)
     prof = ctx.profile_read()
+    pass_ms = ctx.profile_passes()
     ctx.profile(False)
+    log("[bench] per-pass ms (events): " + " ".join(f"{t:.4f}" for t in pass_ms))
+    stream_gbs = ctx.stream_probe(1 << 30, 10)
+    log(f"[bench] streaming read probe: {stream_gbs:.1f} GB/s")
     kname, (kms, kcount) = max(prof.items(), key=lambda kv: kv[1][0])
     avg_ms = kms / kcount
     log("[bench] kernels: " + ", ".join(f"{k_}: {v[0] / v[1] * 1e3:.1f} us x{v[1]}" for k_, v in prof.items()))
@@ -175,14 +223,16 @@ def main():
         achieved = flops / (avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": profile_summary(a.workload),
-                "kernel": kname, "kernel_avg_ms": round(avg_ms, 5)}
+                "kernel": kname, "kernel_avg_ms": round(avg_ms, 5), "flops_per_launch": flops}
     else:
         bytes_alg = float(n) * d * 4
         achieved = bytes_alg / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_summary(a.workload),
-                "kernel": kname, "kernel_avg_ms": round(avg_ms, 5), "bytes_per_launch": bytes_alg}
+                "kernel": kname, "kernel_avg_ms": round(avg_ms, 5), "bytes_per_launch": bytes_alg,
+                "peak_measured": round(stream_gbs, 1), "frac_measured": round(achieved / stream_gbs, 4)}
     cpu = None if a.no_cpu else cpu_baseline(X, C0)
+    cpu2 = None if a.no_cpu else cpu_baseline_numpy(X, C0)
     out = {
         "metric": METRIC,
         "value": round(ms, 5),
@@ -200,9 +250,16 @@ def main():
                    "mode": "exact=False" if a.approx else "exact",
                    "parallelism": "single GPU"},
         "rows_per_s": round(n / (ms * 1e-3)),
+        "pass_ms_events": {"median": round(float(np.median(pass_ms)), 5), "min": round(float(pass_ms.min()), 5),
+                           "max": round(float(pass_ms.max()), 5), "first": round(float(pass_ms[0]), 5),
+                           "passes": int(len(pass_ms)),
+                           "note": "HIP events at every pass boundary of a second timed loop; the first pass of "
+                                   "a fit accumulates every row, later passes only the rows whose label changed"},
+        "stream_read_gbs": round(stream_gbs, 1),
         "final_inertia": inertia,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "cpu_baseline_numpy": cpu2,
     }
     print(json.dumps(out), flush=True)
     ctx.close()

@@ -128,6 +128,17 @@ int32_t km_profile(km_ctx *ctx, int32_t enable);
 int32_t km_profile_read(km_ctx *ctx, int32_t kernel, double *ms_total, int64_t *launches);
 const char *km_kernel_name(int32_t kernel);
 
+/* Per-pass times, in milliseconds, of the km_fit loops run since km_profile(ctx, 1): one HIP event at every pass
+ * boundary on the context's stream. Copies up to cap of them into ms (may be null) and returns how many there
+ * are. The reference times whole fits from the host (bench.py); this reads each pass of one. */
+int64_t km_profile_passes(km_ctx *ctx, double *ms, int64_t cap);
+
+/* Streaming-read probe: the device's HBM read rate for a plain kernel over a fresh `bytes`-byte array (a
+ * multiple of 16, at least 16 MiB), the median of `reps` launches for each of a few grid sizes, the best of
+ * them in GB/s. Replaces quick_bench.py:48-63 (stream_rate), the floor the reference's pass times are read
+ * against. Allocates and frees the array. */
+int32_t km_stream_probe(km_ctx *ctx, int64_t bytes, int32_t reps, double *gbps);
+
 /* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS, _MFMA or _FUSED), and the number of
  * rows in that pass the matrix-core screen could not settle alone: on the fused path (dims 16, 32, 64) rows with
  * more than one centre inside the error window (or non-finite rows), scored against every centre; on the

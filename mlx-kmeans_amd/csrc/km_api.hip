@@ -99,6 +99,7 @@ struct km_ctx {
     std::vector<hipEvent_t> pool;
     double prof_ms[KK_COUNT] = {};
     int64_t prof_n[KK_COUNT] = {};
+    std::vector<double> pass_ms;   // per-pass times of the fit loops run while timing is on
 };
 
 static int fail(km_ctx *c, int code, const char *fmt, ...) {
@@ -808,12 +809,22 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     // only the rows whose label changed
     int rec_pass = 0;
     int pass = 0, relocated = 0;
+    // with timing on, an event at every pass boundary on the stream: the per-pass times km_profile_passes reads
+    std::vector<std::vector<hipEvent_t>> marks;   // per batch: one before each pass, one after the last
+    auto mark = [&](bool first) {
+        if (!c->prof) return;
+        if (first) marks.emplace_back();
+        hipEvent_t e = get_event(c);
+        if (e && hipEventRecord(e, c->stream) == hipSuccess) marks.back().push_back(e);
+    };
     while (pass < max_iter) {
         const int batch = std::min(KM_FIT_BATCH, max_iter - pass);
         for (int i = 0; i < batch; i++) {
             const int lm = !use_ls ? KM_LSTATE_NONE : (pass + i == rec_pass ? KM_LSTATE_RECORD : KM_LSTATE_DELTA);
+            mark(i == 0);
             if ((r = queue_iteration(c, k, mode, path, pass + i, tol, spherical, lm))) return r;
         }
+        mark(false);
         if ((r = read_control(c))) return r;
         pass = c->ctl_h->iter;
         if (c->ctl_h->need_reloc) {
@@ -837,6 +848,14 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     if (last_inertia) *last_inertia = c->ctl_h->inertia;
     if (n_iter) *n_iter = c->ctl_h->iter;
     if (n_relocated) *n_relocated = relocated;
+    // within a batch consecutive marks bracket one pass (between batches the host reads the control block)
+    for (auto &b : marks) {
+        for (size_t i = 0; i + 1 < b.size(); i++) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, b[i], b[i + 1]) == hipSuccess) c->pass_ms.push_back(ms);
+        }
+        for (auto e : b) c->pool.push_back(e);
+    }
     harvest(c);
     return KM_OK;
 }
@@ -1042,6 +1061,7 @@ extern "C" int32_t km_profile(km_ctx *c, int32_t enable) {
         c->prof_ms[i] = 0.0;
         c->prof_n[i] = 0;
     }
+    c->pass_ms.clear();
     c->prof = enable != 0;
     return KM_OK;
 }
@@ -1052,6 +1072,58 @@ extern "C" int32_t km_profile_read(km_ctx *c, int32_t kernel, double *ms_total, 
     harvest(c);
     if (ms_total) *ms_total = c->prof_ms[kernel];
     if (launches) *launches = c->prof_n[kernel];
+    return KM_OK;
+}
+
+extern "C" int64_t km_profile_passes(km_ctx *c, double *ms, int64_t cap) {
+    if (!c) return KM_EINVAL;
+    const int64_t n = (int64_t)c->pass_ms.size();
+    if (ms)
+        for (int64_t i = 0; i < std::min(n, cap); i++) ms[i] = c->pass_ms[i];
+    return n;
+}
+
+extern "C" int32_t km_stream_probe(km_ctx *c, int64_t bytes, int32_t reps, double *gbps) {
+    if (!c) return KM_EINVAL;
+    if (bytes < ((int64_t)1 << 24) || bytes % 16 != 0)
+        return fail(c, KM_EINVAL, "the probe reads a multiple of 16 bytes, at least 16 MiB (got %lld)", (long long)bytes);
+    if (reps < 1 || !gbps) return fail(c, KM_EINVAL, "reps must be positive and gbps not null");
+    HIPCHK(c, hipSetDevice(c->device));
+    const int cfg[] = {2, 4, 8, 16};   // blocks of 256 threads per CU
+    const int max_blocks = c->dev.cus * 16;
+    void *x = nullptr;
+    float *out = nullptr;
+    HIPCHK(c, hipMalloc(&x, (size_t)bytes));
+    hipError_t e = hipMalloc((void **)&out, (size_t)max_blocks * 256 * sizeof(float));
+    hipEvent_t a = nullptr, b = nullptr;
+    if (e == hipSuccess) e = hipMemsetAsync(x, 0, (size_t)bytes, c->stream);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    double best = 0.0;
+    std::vector<float> t(reps);
+    for (int blocks_per_cu : cfg) {
+        const int blocks = c->dev.cus * blocks_per_cu;
+        for (int w = 0; w < 3 && e == hipSuccess; w++) e = km_launch_stream_read(x, bytes, out, blocks, c->stream);
+        for (int i = 0; i < reps && e == hipSuccess; i++) {
+            e = hipEventRecord(a, c->stream);
+            if (e == hipSuccess) e = km_launch_stream_read(x, bytes, out, blocks, c->stream);
+            if (e == hipSuccess) e = hipEventRecord(b, c->stream);
+            if (e == hipSuccess) e = hipEventSynchronize(b);
+            if (e == hipSuccess) e = hipEventElapsedTime(&t[i], a, b);
+        }
+        if (e != hipSuccess) break;
+        std::vector<float> s = t;
+        std::nth_element(s.begin(), s.begin() + reps / 2, s.end());
+        best = std::max(best, (double)bytes / (s[reps / 2] * 1e-3) / 1e9);
+    }
+    (void)hipStreamSynchronize(c->stream);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    (void)hipFree(out);
+    (void)hipFree(x);
+    if (e != hipSuccess)
+        return fail(c, e == hipErrorOutOfMemory ? KM_ENOMEM : KM_EDEVICE, "stream probe failed: %s", hipGetErrorString(e));
+    *gbps = best;
     return KM_OK;
 }
 

@@ -98,6 +98,8 @@ hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb
 hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,
                             int pass, double tol, int flags, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_normalise(float *C, int k, int d, hipStream_t s);
+// Streaming read of `bytes` (a multiple of 16) at x by `blocks` blocks of 256 threads; out holds blocks * 256 floats.
+hipError_t km_launch_stream_read(const void *x, int64_t bytes, float *out, int blocks, hipStream_t s);
 // The reduce and the finish in one launch where the single-block finish serves the shape (the reduce's last block
 // finishes), else the two launches.
 hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,

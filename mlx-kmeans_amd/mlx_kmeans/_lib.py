@@ -41,6 +41,8 @@ SIGNATURES = [
     ("km_last_path", _c.c_int32, [_c.c_void_p]),
     ("km_last_fallback_rows", _c.c_int64, [_c.c_void_p]),
     ("km_version", _c.c_int32, []),
+    ("km_profile_passes", _c.c_int64, [_c.c_void_p, _f64p, _c.c_int64]),
+    ("km_stream_probe", _c.c_int32, [_c.c_void_p, _c.c_int64, _c.c_int32, _f64p]),
     ("km_pass_noalloc", _c.c_int32, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int32, _c.c_void_p, _c.c_int32,
                                      _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p]),
 ]
@@ -187,6 +189,21 @@ class Context:
                 out[name] = (ms.value, cnt.value)
             i += 1
         return out
+
+    def profile_passes(self):
+        """-> float64 array of per-pass milliseconds of the fit loops run since profile(True)."""
+        L = lib()
+        n = int(L.km_profile_passes(self._h, None, 0))
+        out = np.zeros(max(n, 1), np.float64)
+        if n:
+            L.km_profile_passes(self._h, _ptr(out, ctypes.c_double), n)
+        return out[:n]
+
+    def stream_probe(self, nbytes=1 << 30, reps=10):
+        """-> GB/s of a plain streaming read of a fresh nbytes array (the best grid's median of reps)."""
+        g = ctypes.c_double()
+        self._check(lib().km_stream_probe(self._h, int(nbytes), int(reps), ctypes.byref(g)))
+        return g.value
 
     def last_path(self):
         return {KM_PATH_ROWS: "rows", KM_PATH_MFMA: "mfma", KM_PATH_FUSED: "fused"}.get(
