@@ -365,7 +365,7 @@ static int ensure_pass_buffers(km_ctx *c, int k, size_t total_rb, bool need_rows
     HIPCHK(c, c->psum.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)kw));
     HIPCHK(c, c->tot.ensure((size_t)kw));
-    HIPCHK(c, c->red.ensure((size_t)km_reduce_splits((int)total_rb, kw) * kw));
+    HIPCHK(c, c->red.ensure((size_t)km_reduce_splits((int)total_rb, kw, c->dev.cus) * kw));
     if (need_rows_scratch) {
         HIPCHK(c, c->labels.ensure((size_t)c->n));
         HIPCHK(c, c->best.ensure((size_t)c->n));
@@ -381,7 +381,7 @@ static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags
     const int64_t kw = (int64_t)k * (d + 2);
     float *Cn = c->Cb[(pass + 1) & 1].p;
     if (!presummed) {
-        const int S = km_reduce_splits(rb, kw);
+        const int S = km_reduce_splits(rb, kw, c->dev.cus);
         HIPCHK(c, launch(c, KK_REDUCE, [&] {
             return km_launch_reduce_finish(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, k, d, c->tot.p, Cn, c->ctl, pass,
                                            tol, flags, stop, c->stream);
@@ -642,7 +642,7 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
         HIPCHK(c, c->psum.ensure(total_rb * (size_t)k * 2));
         HIPCHK(c, c->pcomp.ensure(total_rb * (size_t)k * 2));
         HIPCHK(c, c->tot2.ensure((size_t)k * 2));
-        const int S2 = km_reduce_splits((int)total_rb, (int64_t)k * 2);
+        const int S2 = km_reduce_splits((int)total_rb, (int64_t)k * 2, c->dev.cus);
         HIPCHK(c, c->red.ensure((size_t)S2 * k * 2));
         int rb = 0;
         int64_t row0 = 0;
@@ -945,7 +945,7 @@ struct ScratchCarve {
 
 // Bytes of scratch the reduce + finish of nrb partials of kw entries use (partials included).
 static size_t na_reduce_bytes(int nrb, int64_t kw) {
-    const int S = km_reduce_splits(nrb, kw);
+    const int S = km_reduce_splits(nrb, kw, 1 << 30);   // the most range sums any device's split takes
     auto r = [](size_t b) { return (b + 255) / 256 * 256; };
     return 2 * r((size_t)nrb * kw * sizeof(float)) + r((size_t)S * kw * sizeof(double));
 }
@@ -1016,7 +1016,7 @@ extern "C" int32_t km_pass_noalloc(km_ctx *c, const float *X, int64_t rows, int3
         ap = km_plan_accum_generic(rows, d, k, maxb);
         nrb = ap.nrb;
     }
-    const int S = km_reduce_splits(nrb, kw);
+    const int S = km_reduce_splits(nrb, kw, c->dev.cus);
     float *psum = nullptr, *pcomp = nullptr;
     double *red = nullptr;
     if (!sc.take(&psum, (size_t)nrb * kw) || !sc.take(&pcomp, (size_t)nrb * kw) || !sc.take(&red, (size_t)S * kw))
@@ -1036,7 +1036,7 @@ extern "C" int32_t km_pass_noalloc(km_ctx *c, const float *X, int64_t rows, int3
     HIPCHK(c, km_launch_reduce_finish(psum, pcomp, nrb, kw, S, red, k, d, totals, nullptr, ctl, 0, 0.0, 0, nullptr, s));
     if (fam == FAM_MFMA_FUSED) {
         // per-cluster best sums: [count, best] accumulated from this pass's labels and best (as km_pass does)
-        const int S2 = km_reduce_splits(p2.nrb, kw2);
+        const int S2 = km_reduce_splits(p2.nrb, kw2, c->dev.cus);
         float *ps2 = nullptr, *pc2 = nullptr;
         double *red2 = nullptr, *tot2 = nullptr;
         if (!sc.take(&ps2, (size_t)p2.nrb * kw2) || !sc.take(&pc2, (size_t)p2.nrb * kw2) ||

@@ -226,10 +226,13 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
 // beyond, one block per cluster (k_finish) and one block for the statistics (k_stats).
 
 static constexpr int KM_FIN1_MAX = 4096;   // entries k * (d + 2) finished by a single block (LDS)
-static constexpr int KM_FIN1_SPLITS = 16;  // range sums read per entry by the single block
+static constexpr int KM_FIN1_SPLITS = 8;   // range sums read per entry by the single block
 
-int km_reduce_splits(int nrb, int64_t kw) {
-    const int cap = kw <= KM_FIN1_MAX ? KM_FIN1_SPLITS : 64;
+int km_reduce_splits(int nrb, int64_t kw, int cus) {
+    int cap = kw <= KM_FIN1_MAX ? KM_FIN1_SPLITS : 64;
+    // one 1024-thread block per CU at a time: keep the grid (entries / 64 x splits) within one round of blocks
+    const int64_t cols = (kw + 63) / 64;
+    if (kw <= KM_FIN1_MAX && cols * cap > cus) cap = (int)std::max<int64_t>(1, cus / cols);
     int s = nrb / 16;
     if (s > cap) s = cap;
     if (s < 1) s = 1;
@@ -280,13 +283,26 @@ hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb
 // The pass statistics from the totals (counts in column 0, best sums in column 1), by `nthreads` threads of
 // one block: strided per-thread sums over clusters ascending, then a fixed tree. Writes the control block and
 // gives still-empty clusters (when no relocation is due) the largest cluster's centre.
+// (count, index) pairs: the larger count wins, the smaller index on a tie
+__device__ inline void max_pair(long long &mx, int &arg, long long mo, int ao) {
+    if (mo > mx || (mo == mx && ao < arg)) {
+        mx = mo;
+        arg = ao;
+    }
+}
+
+// Statistics of a pass from its totals: inertia, empty clusters, the largest cluster (first on a tie), and the
+// stop flags. Each thread folds a strided set of clusters, each wave folds its lanes with a butterfly (every lane
+// ends with the same bits: each step adds the same two values), and wave 0 folds the waves: two barriers.
 template <int NT>
 __device__ void pass_stats(const double *tot, int k, int d, float *Cnext, km_control *ctl, int pass, double tol) {
-    const int tid = threadIdx.x, W = d + 2;
-    __shared__ double s_in[NT];
-    __shared__ int s_empty[NT];
-    __shared__ long long s_max[NT];
-    __shared__ int s_arg[NT];
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, W = d + 2, lane = tid & 63, wave = tid >> 6;
+    __shared__ double s_in[NW];
+    __shared__ int s_empty[NW];
+    __shared__ long long s_max[NW];
+    __shared__ int s_arg[NW];
+    __shared__ int s_res[2];
     double in = 0.0;
     int empty = 0;
     long long mx = -1;
@@ -295,40 +311,51 @@ __device__ void pass_stats(const double *tot, int k, int d, float *Cnext, km_con
         const long long n_c = llrint(tot[(int64_t)cc * W]);
         in += tot[(int64_t)cc * W + 1];
         empty += n_c == 0;
-        if (n_c > mx) { mx = n_c; arg = cc; }   // strided ascending cc: the first maximum within this thread
+        max_pair(mx, arg, n_c, cc);
     }
-    s_in[tid] = in;
-    s_empty[tid] = empty;
-    s_max[tid] = mx;
-    s_arg[tid] = arg;
+    for (int off = 32; off > 0; off >>= 1) {
+        in += __shfl_xor(in, off);
+        empty += __shfl_xor(empty, off);
+        max_pair(mx, arg, __shfl_xor(mx, off), __shfl_xor(arg, off));
+    }
+    if (lane == 0) {
+        s_in[wave] = in;
+        s_empty[wave] = empty;
+        s_max[wave] = mx;
+        s_arg[wave] = arg;
+    }
     __syncthreads();
-    for (int h = NT / 2; h > 0; h >>= 1) {
-        if (tid < h) {
-            s_in[tid] += s_in[tid + h];
-            s_empty[tid] += s_empty[tid + h];
-            const long long mo = s_max[tid + h];
-            const int ao = s_arg[tid + h];
-            if (mo > s_max[tid] || (mo == s_max[tid] && ao < s_arg[tid])) { s_max[tid] = mo; s_arg[tid] = ao; }
+    if (wave == 0) {
+        in = lane < NW ? s_in[lane] : 0.0;
+        empty = lane < NW ? s_empty[lane] : 0;
+        mx = lane < NW ? s_max[lane] : -1;
+        arg = lane < NW ? s_arg[lane] : 0;
+        for (int off = NW / 2; off > 0; off >>= 1) {
+            in += __shfl_xor(in, off);
+            empty += __shfl_xor(empty, off);
+            max_pair(mx, arg, __shfl_xor(mx, off), __shfl_xor(arg, off));
         }
-        __syncthreads();
+        if (lane == 0) {
+            const double inertia = in;
+            const int need_reloc = (empty > 0 && inertia > 0.0) ? 1 : 0;
+            int done = 0;
+            if (pass > 0 && fabs(ctl->prev - inertia) <= tol * ctl->prev) done = 1;
+            ctl->prev = inertia;
+            ctl->inertia = inertia;
+            ctl->n_empty = empty;
+            ctl->big = arg;
+            ctl->need_reloc = need_reloc;
+            ctl->done = done;
+            ctl->iter = pass + 1;
+            // a non-finite inertia (NaN or overflowing data) ends the loop at once: the caller explains it
+            ctl->stop = (done || need_reloc || !isfinite(inertia)) ? 1 : 0;
+            s_res[0] = (empty > 0 && !need_reloc) ? 1 : 0;
+            s_res[1] = arg;
+        }
     }
-    const double inertia = s_in[0];
-    const int ne = s_empty[0], big = s_arg[0];
-    const int need_reloc = (ne > 0 && inertia > 0.0) ? 1 : 0;
-    if (tid == 0) {
-        int done = 0;
-        if (pass > 0 && fabs(ctl->prev - inertia) <= tol * ctl->prev) done = 1;
-        ctl->prev = inertia;
-        ctl->inertia = inertia;
-        ctl->n_empty = ne;
-        ctl->big = big;
-        ctl->need_reloc = need_reloc;
-        ctl->done = done;
-        ctl->iter = pass + 1;
-        // a non-finite inertia (NaN or overflowing data) ends the loop at once: the caller explains it
-        ctl->stop = (done || need_reloc || !isfinite(inertia)) ? 1 : 0;
-    }
-    if (ne > 0 && !need_reloc) {
+    __syncthreads();
+    if (s_res[0]) {   // empty clusters with zero inertia: they take the largest cluster's centre
+        const int big = s_res[1];
         for (int cc = 0; cc < k; cc++) {
             if (llrint(tot[(int64_t)cc * W]) != 0) continue;
             for (int j = tid; j < d; j += NT) Cnext[(int64_t)cc * d + j] = Cnext[(int64_t)big * d + j];
@@ -356,19 +383,30 @@ __device__ void finish1_body(const double *__restrict__ tmp, int S, int k, int d
                              double *Ts) {
     const int tid = threadIdx.x, W = d + 2;
     const int kw = k * W;
-    for (int e = tid; e < kw; e += 1024) {
-        double v[KM_FIN1_SPLITS];
+    constexpr int PER = KM_FIN1_MAX / 1024;   // entries per thread
+    // every load first (one round of memory latency), then the fixed-order sums
+    double v[PER][KM_FIN1_SPLITS], prev[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int e = tid + 1024 * i;
 #pragma unroll
         for (int sp = 0; sp < KM_FIN1_SPLITS; sp++) {
             double *src = const_cast<double *>(tmp) + (int64_t)sp * kw + e;
-            v[sp] = sp < S ? (COHERENT ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *src)
+            v[i][sp] = (e < kw && sp < S)
+                           ? (COHERENT ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *src)
                            : 0.0;
         }
-        double t = v[0];
+        prev[i] = (e < kw && (flags & KM_FIN_DELTA)) ? tot[e] : 0.0;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int e = tid + 1024 * i;
+        if (e >= kw) continue;
+        double t = v[i][0];
 #pragma unroll
         for (int sp = 1; sp < KM_FIN1_SPLITS; sp++)
-            if (sp < S) t += v[sp];
-        if ((flags & KM_FIN_DELTA) && e % W != 1) t = tot[e] + t;   // the previous totals plus their change
+            if (sp < S) t += v[i][sp];
+        if ((flags & KM_FIN_DELTA) && e % W != 1) t = prev[i] + t;   // the previous totals plus their change
         Ts[e] = t;
         tot[e] = t;
     }

@@ -85,7 +85,7 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
                                    float *pcomp, int rb0, const int32_t *stop, hipStream_t s);
 
 // Partials (nrb, k*w) sum+comp -> float64 sums of S = km_reduce_splits(nrb, k*w) fixed ranges: tmp (S, k*w).
-int km_reduce_splits(int nrb, int64_t kw);
+int km_reduce_splits(int nrb, int64_t kw, int cus);
 hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
                                   const int32_t *stop, hipStream_t s);
 

@@ -446,14 +446,18 @@ def test_embed_workload_full_size(lib):
     ctx.close()
 
 
-@pytest.mark.parametrize("d,k,parts", [(32, 64, 1), (16, 40, 2), (64, 32, 1), (32, 20, 3), (16, 64, 1)])
-def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts):
+@pytest.mark.parametrize("d,k,parts,path", [(32, 64, 1, "mfma"), (16, 40, 2, "mfma"), (64, 32, 1, "mfma"),
+                                            (32, 20, 3, "mfma"), (16, 64, 1, "mfma"), (4, 12, 1, "fused"),
+                                            (8, 8, 2, "fused"), (2, 40, 1, "fused"), (3, 30, 3, "fused"),
+                                            (16, 8, 1, "fused"), (1, 200, 1, "fused")])
+def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts, path):
     """The fit loop accumulates, after its first pass, only the rows whose label changed (into the new cluster, out of
     the old one) and adds that to the previous pass's totals. The same number of Lloyd steps run one at a time with
     a full accumulation each (km_lloyd_step) must reach the same centres (within 1e-6 of the RMS) and inertia
     (within 1e-6), with the same iteration count under a tolerance; reruns of the loop are bit-identical. The data
     keep rows moving between clusters for several passes (overlapping blobs, starting centres drawn from one
-    corner)."""
+    corner). On the fused matrix-core path ("mfma") the loop accumulates only changed rows; on the fused low-d path
+    ("fused", with and without the screen) it accumulates every row each pass, and must agree all the same."""
     rng = np.random.default_rng(900 + d + k + parts)
     n = 90_011
     cen = rng.uniform(-3, 3, size=(k, d)).astype(np.float32)
@@ -469,6 +473,7 @@ def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts):
     say(f"[gpu] change accumulation d={d} k={k} parts={parts}")
     C_fit, in_fit, it_fit, _ = ctx.fit(C0, steps, -1.0)
     assert it_fit == steps
+    assert ctx.last_path() == path
     C = C0
     moved = []
     prev_lab = None
