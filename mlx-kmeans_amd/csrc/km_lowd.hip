@@ -4,7 +4,7 @@
 //
 // Assignment. Each lane owns whole rows. Without the screen it runs the rows loop itself (core.py:263-274): for
 // every centre in ascending order, s = sum_j (x_j - c_j)^2 with j ascending, product and add rounded separately,
-// kept when s < best. With the screen (k >= 24) it first computes the expanded form a_c = |c|^2 - 2 x.c for every
+// kept when s < best. With the screen (k >= 8) it first computes the expanded form a_c = |c|^2 - 2 x.c for every
 // centre as a float32 FMA chain (d FMAs instead of the direct form's 3d operations), keeps the smallest and second
 // smallest key (the centre index packed into the low mantissa bits), and proves with a rigorous error window that
 // no other centre can hold the row's minimum; the direct form then runs on that one centre only. Rows the window
@@ -32,11 +32,12 @@
 #include "km_internal.h"
 #include <math.h>
 
-template <int D>
+template <int D, bool SCR>
 struct LowGeo {
     static constexpr int W = D + 2;                                // columns: count, best, dims
-    // rows per lane per iteration: the loads in flight while the previous rows are scored
-    static constexpr int R = D <= 8 ? 8 : 4;
+    // rows per lane per iteration: the loads in flight while the previous rows are scored (the screen keeps the
+    // shifted rows too, so above 4 dims it holds four rows to stay within three waves' registers)
+    static constexpr int R = SCR ? (D <= 4 ? 8 : 4) : (D <= 8 ? 8 : 4);
     static constexpr int FOLD_ROWS = 256;                          // additions per tile column between folds
     static constexpr int FOLD_IT = FOLD_ROWS / R;                  // iterations between folds with private columns
 };
@@ -44,11 +45,11 @@ struct LowGeo {
 __host__ __device__ constexpr size_t km_al16(size_t v) { return (v + 15) / 16 * 16; }
 
 // LDS bytes of one block (one wave): centres, the 64 >> lsh tiles, the float64 accumulators, and with the
-// screen the centres as [-2c, |c|^2] rows
+// screen the centres as [-2c, |c|^2] rows and once more dimension-major (the per-row gathers of one centre each)
 __host__ __device__ inline size_t km_lowd_lds(int d, int k, bool screen, int lsh) {
     const size_t kw = (size_t)k * (d + 2);
     return km_al16((size_t)k * d * 4) + kw * (64 >> lsh) * 4 + kw * 8 +
-           (screen ? km_al16((size_t)k * (d + 1) * 4) : 0);
+           (screen ? km_al16((size_t)k * (d + 1) * 4) + km_al16((size_t)k * d * 4) : 0);
 }
 
 __host__ __device__ constexpr double km_lowd_gamma(int m) {
@@ -58,6 +59,13 @@ __host__ __device__ constexpr double km_lowd_gamma(int m) {
 __device__ __forceinline__ float lowd_vmin(float a, float b) {
     float r;
     asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// a with its low index bits replaced by c: (mask & c) | (~mask & a) in one v_bfi_b32 (the mask in a VGPR, the
+// wave-uniform index in an SGPR)
+__device__ __forceinline__ float lowd_key(float a, uint32_t mask_v, uint32_t c) {
+    float r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask_v), "s"(c), "v"(a));
     return r;
 }
 // v_min3_f32: two v_min_f32 in a row by definition (the same result for every input, NaN included)
@@ -70,15 +78,12 @@ __device__ __forceinline__ float lowd_vmin3(float a, float b, float c) {
 // Largest k * (d + 2) served: the shared tiles (64 bytes per entry), the float64 accumulators (8) and the centres
 // (under 8) stay within 64 KB of LDS.
 static constexpr int KM_LOWD_MAX_KW = 768;
-// Shared tile columns: 4 lanes take turns on each of 16 columns (the fold interval (256 / R) >> 2 stays at
-// least one iteration for every R <= 16).
-static constexpr int KM_LOWD_SHARED_LSH = 2;
-// Shared columns cost four LDS read-modify-write passes per iteration instead of one; they pay only when the
-// private layout leaves few waves per CU or few row bytes in flight per CU (measured on MI355X, 20M rows: d = 8,
-// k = 12: 531 -> 214 us with 4 private waves; d = 4, k = 16: 171 -> 137 us with 6; d = 2, k = 16: 102 -> 86 us
-// with 9 waves holding 36 KB; but d = 8, k = 8 with 7 waves holding 112 KB: private 154 us, shared 173 us).
-static constexpr int KM_LOWD_PRIVATE_MIN_WAVES = 6;
-static constexpr int64_t KM_LOWD_PRIVATE_MIN_BYTES = 48 * 1024;
+// Tile columns: 64 >> lsh, with 1 << lsh lanes taking turns on each (lsh = 0, 1, 2; the fold interval
+// (256 / R) >> lsh stays at least one iteration for every R <= 16). Sharing costs one LDS read-modify-write pass
+// per lane group and buys occupancy where the tiles, not the registers, limit it; the plan takes the least
+// sharing that reaches the highest occupancy (measured on MI355X: 96M x 4, k = 12 with the screen: private 8
+// waves per CU 465 us, two lanes per column 12 waves 417 us; 10M x 8, k = 8: 7 waves 90 us, 12 waves 85 us).
+static constexpr int KM_LOWD_MAX_LSH = 2;
 
 template <int D>
 __device__ __forceinline__ void load_row(const float *__restrict__ X, int64_t row, float (&x)[D]) {
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                                                    uint32_t *__restrict__ labels, float *__restrict__ best,
                                                    float *__restrict__ psum, float *__restrict__ pcomp, int rb0,
                                                    const int32_t *__restrict__ stop) {
-    using G = LowGeo<D>;
+    using G = LowGeo<D, SCR>;
     constexpr int W = G::W, R = G::R;
     // Window constants, in coordinates shifted by o (the centres' mean): x' = fl(x - o), c' = fl(c - o). The screen
     // a'_c = |c'|^2 - 2 x'.c' (FMA chain) is within E <= gE (|c'|^2 + 2 |x'||c'|) <= gE (2 max|c'|^2 + |x'|^2) of
@@ -157,8 +162,11 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
     float *T = lds + km_al16((size_t)k * D * 4) / 4;                      // [kw][L]
     double *F = reinterpret_cast<double *>(T + (size_t)kw * L);           // [kw]
     float *Q = reinterpret_cast<float *>(F + kw);                         // [k][D + 1]: -2c, |c|^2 (screen)
-
+    float *Ct = Q + km_al16((size_t)k * (D + 1) * 4) / 4;                // [D][k] (screen): lanes gathering
+                                                                          // different centres hit different banks
     for (int e = lane; e < k * D; e += 64) Cl[e] = C[e];
+    if constexpr (SCR)
+        for (int e = lane; e < k * D; e += 64) Ct[(e % D) * k + e / D] = C[e];
     for (int e = lane; e < kw * L; e += 64) T[e] = 0.0f;
     for (int e = lane; e < kw; e += 64) F[e] = 0.0;
     // screen constants: the shift o, max |c'| (rounded up), max |c'|^2, and the index bits packed into keys
@@ -193,6 +201,7 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
         while ((1 << ib) < k) ib++;
     }
     const uint32_t imask = (1u << ib) - 1u;
+    const uint32_t imask_v = __builtin_amdgcn_readfirstlane(imask);
     const float rho = (float)(1.01 * (double)(1 << ib) * 0x1p-23);
     const float csq2 = fmaxf(csqmax, cnmax * cnmax) * 2.0f * (1.0f + 0x1p-20f);
     const float w_c = (float)((2.0 * gE + 2.0 * gd * gE) * (1.0 + 0x1p-18)) * csq2 + 4.0f * TINY;
@@ -216,10 +225,16 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
         const int64_t r1 = r0 + STEP;
         const bool more = r1 < r_end;
         if (more) {
+            if (r1 + STEP <= r_end) {   // the whole next step in range: one base address, constant offsets
+                const float *xb = X + (r1 + lane) * D;
 #pragma unroll
-            for (int i = 0; i < R; i++) {
-                const int64_t row = r1 + 64 * i + lane;
-                load_row<D>(X, row < r_end ? row : r_end - 1, xn[i]);
+                for (int i = 0; i < R; i++) load_row<D>(xb + (int64_t)64 * D * i, 0, xn[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    const int64_t row = r1 + 64 * i + lane;
+                    load_row<D>(X, row < r_end ? row : r_end - 1, xn[i]);
+                }
             }
         }
         float bst[R];
@@ -252,8 +267,8 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                         a = __builtin_fmaf(xs[i][j], q[j], a);
                         b = __builtin_fmaf(xs[i][j], p[j], b);
                     }
-                    const float ka = __uint_as_float((__float_as_uint(a) & ~imask) | (uint32_t)c);
-                    const float kb = __uint_as_float((__float_as_uint(b) & ~imask) | (uint32_t)(c + 1));
+                    const float ka = lowd_key(a, imask_v, (uint32_t)c);
+                    const float kb = lowd_key(b, imask_v, (uint32_t)(c + 1));
                     m2[i] = lowd_vmin(m2[i], __builtin_amdgcn_fmed3f(m1[i], ka, kb));
                     m1[i] = lowd_vmin3(m1[i], ka, kb);
                 }
@@ -267,7 +282,7 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                     float a = q[D];
 #pragma unroll
                     for (int j = 0; j < D; j++) a = __builtin_fmaf(xs[i][j], q[j], a);
-                    const float key = __uint_as_float((__float_as_uint(a) & ~imask) | (uint32_t)c);
+                    const float key = lowd_key(a, imask_v, (uint32_t)c);
                     m2[i] = __builtin_amdgcn_fmed3f(m1[i], m2[i], key);
                     m1[i] = lowd_vmin(m1[i], key);
                 }
@@ -290,7 +305,7 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                 float s = 0.0f;
 #pragma unroll
                 for (int j = 0; j < D; j++) {
-                    const float t = xr[i][j] - Cl[cmc * D + j];
+                    const float t = xr[i][j] - Ct[j * k + cmc];
                     s = s + t * t;
                 }
                 // settled: no second centre inside the window, a finite row (xsq) and distance, an index below k
@@ -320,7 +335,7 @@ __global__ __launch_bounds__(64) void k_fused_lowd(const float *__restrict__ X, 
                         float sc = 0.0f;
 #pragma unroll
                         for (int j = 0; j < D; j++) {
-                            const float t = xb[j] - Cl[c * D + j];
+                            const float t = xb[j] - Ct[j * k + c];
                             sc = sc + t * t;
                         }
                         if (sc < bv) {
@@ -429,17 +444,18 @@ typedef void (*lowd_fn)(const float *, int64_t, const float *, int, int64_t, uin
      k_fused_lowd<8, S, H>,  k_fused_lowd<9, S, H>,  k_fused_lowd<10, S, H>, k_fused_lowd<11, S, H>,             \
      k_fused_lowd<12, S, H>, k_fused_lowd<13, S, H>, k_fused_lowd<14, S, H>, k_fused_lowd<15, S, H>,             \
      k_fused_lowd<16, S, H>}
-// [screen][shared columns][dims]
-static lowd_fn g_lowd[2][2][17] = {{KM_LOWD_FNS(false, 0), KM_LOWD_FNS(false, KM_LOWD_SHARED_LSH)},
-                                   {KM_LOWD_FNS(true, 0), KM_LOWD_FNS(true, KM_LOWD_SHARED_LSH)}};
+// [screen][lsh][dims]
+static lowd_fn g_lowd[2][KM_LOWD_MAX_LSH + 1][17] = {
+    {KM_LOWD_FNS(false, 0), KM_LOWD_FNS(false, 1), KM_LOWD_FNS(false, 2)},
+    {KM_LOWD_FNS(true, 0), KM_LOWD_FNS(true, 1), KM_LOWD_FNS(true, 2)}};
 #undef KM_LOWD_FNS
 
-static int lowd_rows_per_iter(int d) { return 64 * (d <= 8 ? 8 : 4); }
+static int lowd_rows_per_iter(int d, bool scr) { return 64 * (scr ? (d <= 4 ? 8 : 4) : (d <= 8 ? 8 : 4)); }
 
-// The screen costs d + 3 operations per centre and row against the direct form's 3d + 3, plus a per-row window
-// and one direct form with an LDS gather; measured on MI355X it is the faster of the two from about 24 centres on
-// (20M rows: d = 4, k = 32 -21 %; d = 2, k = 48 -15 %) and not below (d = 4, k = 12 +5 %; d = 8, k = 8 +1 %).
-static bool lowd_screen(int k) { return k >= 24; }
+// The screen costs d + 2.5 operations per centre and row against the direct form's 3d + 3, plus a per-row window
+// and one direct form with an LDS gather; measured on MI355X it is the faster of the two from about 8 centres on
+// (96M x 4, k = 12: 465 against 471 us private, 417 with shared columns; 10M x 8, k = 8: 85 against 90 us).
+static bool lowd_screen(int k) { return k >= 8; }
 
 km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bool aligned, int64_t max_blocks) {
     km_lowd_plan pl{};
@@ -447,23 +463,22 @@ km_lowd_plan km_plan_lowd(const km_device_info &dev, int64_t n, int d, int k, bo
     if ((int64_t)k * (d + 2) > KM_LOWD_MAX_KW) return pl;
     if ((d % 2 == 0) && !aligned) return pl;   // vector row loads need 8/16-byte aligned rows
     const bool scr = lowd_screen(k);
-    // private tile columns unless sharing them lets more waves reside (LDS- rather than register-bound)
-    int occs[2] = {0, 0};
-    for (int h = 0; h < 2; h++) {
-        const size_t b = km_lowd_lds(d, k, scr, h ? KM_LOWD_SHARED_LSH : 0);
-        if (b > 65536 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&occs[h], (const void *)g_lowd[scr][h][d], 64,
-                                                                      b) != hipSuccess)
-            occs[h] = 0;
+    // the least column sharing that reaches the highest occupancy
+    int lsh = -1, occ = 0;
+    for (int h = 0; h <= KM_LOWD_MAX_LSH; h++) {
+        const size_t b = km_lowd_lds(d, k, scr, h);
+        int o = 0;
+        if (b > 65536 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, (const void *)g_lowd[scr][h][d], 64, b) !=
+                             hipSuccess)
+            o = 0;
+        if (o > occ) {
+            occ = o;
+            lsh = h;
+        }
     }
-    const int shared = occs[1] > occs[0] && (occs[0] <= KM_LOWD_PRIVATE_MIN_WAVES ||
-                                             (int64_t)occs[0] * lowd_rows_per_iter(d) * d * 4 < KM_LOWD_PRIVATE_MIN_BYTES)
-                           ? 1
-                           : 0;
-    const int occ = occs[shared];
     if (occ < 1) return pl;
-    const int lsh = shared ? KM_LOWD_SHARED_LSH : 0;
     const size_t lds = km_lowd_lds(d, k, scr, lsh);
-    const int64_t unit = lowd_rows_per_iter(d);
+    const int64_t unit = lowd_rows_per_iter(d, scr);
     const int64_t units = (n + unit - 1) / unit;
     int64_t nrb = (int64_t)dev.cus * occ;
     if (nrb > units) nrb = units;
@@ -484,7 +499,7 @@ hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s) {
     if (!pl.ok || d < 1 || d > 16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(g_lowd[pl.screen ? 1 : 0][pl.lsh ? 1 : 0][d], dim3(pl.nrb), dim3(64), pl.lds, s, X, n, C, k,
+    hipLaunchKernelGGL(g_lowd[pl.screen ? 1 : 0][pl.lsh][d], dim3(pl.nrb), dim3(64), pl.lds, s, X, n, C, k,
                        pl.rbs, labels, best, psum, pcomp, rb0, stop);
     return hipGetLastError();
 }
