@@ -7,9 +7,9 @@
 //   ->  k_finish (totals; new centres into the other buffer; in its last block the statistics and stopping rule)
 // Pass p reads centre buffer p % 2 and writes buffer (p + 1) % 2. The loop state lives in a device-side
 // km_control block and every kernel of a pass is gated on it, so km_fit queues iterations back to back and looks
-// at the state only every KM_FIT_BATCH iterations. A pass that leaves clusters empty stops the queue; the host
+// at the state only every KM_FIT_BATCH iterations. A pass that leaves clusters empty stops the queue; the device
 // then relocates them the way the reference's lloyd_step does (core.py:2222-2242), from that pass's input
-// centres and totals, and resumes.
+// centres and totals, and the loop resumes.
 #include "kmeans_hip.h"
 #include "km_internal.h"
 
@@ -90,6 +90,11 @@ struct km_ctx {
     DBuf<float> best;
     DBuf<float> pp_S, pp_C;     // k-means++: the row sample (transposed, dims x m) and the picked rows
     DBuf<int64_t> pp_idx;       // k-means++: the sample's row indices, local to their slice
+    DBuf<uint32_t> rl_st, rl_tie;   // relocation: selection state and per-block tie counts
+    DBuf<int32_t> rl_empty;         // relocation: the empty clusters, ascending
+    DBuf<int64_t> rl_sel;           // relocation: the taken rows, then in order
+    DBuf<double> rl_ws;             // relocation: the patched totals
+    DBuf<char> rl_parts;            // relocation: the slice table
     DBuf<char> pp_ws;           // k-means++: the rounds' workspace
     km_control *ctl = nullptr;    // device
     km_control *ctl_h = nullptr;  // pinned host mirror
@@ -241,6 +246,12 @@ extern "C" void km_destroy(km_ctx *c) {
     c->pp_C.release();
     c->pp_idx.release();
     c->pp_ws.release();
+    c->rl_st.release();
+    c->rl_tie.release();
+    c->rl_empty.release();
+    c->rl_sel.release();
+    c->rl_ws.release();
+    c->rl_parts.release();
     for (auto &r : c->recs) {
         (void)hipEventDestroy(r.a);
         (void)hipEventDestroy(r.b);
@@ -671,75 +682,43 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
     return KM_OK;
 }
 
-// ------------------------------------------------------------------ relocation of empty clusters (host side)
+// ------------------------------------------------------------------ relocation of empty clusters
 //
 // The pass `pass` whose statistics flagged empties left its totals in c->tot and its input centres in
 // Cb[pass & 1]; the relocated centres go to Cb[(pass + 1) & 1].
 // Following lloyd_step (core.py:2222-2242): the empty clusters, in ascending order, take the rows with the
 // largest best distance (ties: lower row index); each such row leaves its old cluster; centres are the
-// float64 means rounded to float32; a cluster still empty takes the largest cluster's centre.
+// float64 means rounded to float32; a cluster still empty takes the largest cluster's centre. All of it runs on
+// the device (km_reloc.hip): the host reads back only the number of empty clusters.
 static int relocate(km_ctx *c, int k, int mode, int path, int pass, int *n_empty_out) {
-    const int d = c->d, w = d + 2;
-    std::vector<double> tot((size_t)k * w);
-    HIPCHK(c, hipMemcpyAsync(tot.data(), c->tot.p, tot.size() * sizeof(double), hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    std::vector<int64_t> counts(k);
-    std::vector<double> sums((size_t)k * d);
-    std::vector<int> empty;
-    for (int j = 0; j < k; j++) {
-        counts[j] = llrint(tot[(size_t)j * w]);
-        for (int e = 0; e < d; e++) sums[(size_t)j * d + e] = tot[(size_t)j * w + 2 + e];
-        if (counts[j] == 0) empty.push_back(j);
+    const int d = c->d;
+    if (c->n > (int64_t)UINT32_MAX)
+        return fail(c, KM_EINVAL, "relocating empty clusters counts rows in 32 bits: %lld rows is too many",
+                    (long long)c->n);
+    int r = run_labels(c, k, mode, path, pass);
+    if (r) return r;
+    const int64_t nb = km_reloc_blocks(c->n, c->dev.cus);
+    HIPCHK(c, c->rl_st.ensure(km_reloc_state_words()));
+    HIPCHK(c, c->rl_empty.ensure((size_t)k));
+    HIPCHK(c, c->rl_sel.ensure(2 * (size_t)k));
+    HIPCHK(c, c->rl_tie.ensure((size_t)nb));
+    HIPCHK(c, c->rl_ws.ensure((size_t)k * (d + 2)));
+    HIPCHK(c, c->rl_parts.ensure(c->parts.size() * 16));
+    std::vector<const float *> px;
+    std::vector<int64_t> pr;
+    for (auto &p : c->parts) {
+        px.push_back(p.X);
+        pr.push_back(p.rows);
     }
-    *n_empty_out = (int)empty.size();
-    if (!empty.empty()) {
-        int r = run_labels(c, k, mode, path, pass);
-        if (r) return r;
-        std::vector<float> best(c->n);
-        std::vector<uint32_t> labels(c->n);
-        HIPCHK(c, hipMemcpyAsync(best.data(), c->best.p, c->n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
-        HIPCHK(c, hipMemcpyAsync(labels.data(), c->labels.p, c->n * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
-        HIPCHK(c, hipStreamSynchronize(c->stream));
-        float bmax = 0.0f;
-        for (float b : best) bmax = std::max(bmax, b);
-        if (bmax > 0.0f) {
-            const int64_t m = std::min<int64_t>((int64_t)empty.size(), c->n);
-            std::vector<int64_t> idx(c->n);
-            for (int64_t i = 0; i < c->n; i++) idx[i] = i;
-            auto farther = [&](int64_t a, int64_t b) { return best[a] > best[b] || (best[a] == best[b] && a < b); };
-            std::partial_sort(idx.begin(), idx.begin() + m, idx.end(), farther);
-            std::vector<float> row(d);
-            for (int64_t t = 0; t < m; t++) {
-                const int64_t f = idx[t];
-                // locate row f in its slice
-                int64_t off = f;
-                const float *src = nullptr;
-                for (auto &p : c->parts) {
-                    if (off < p.rows) { src = p.X + off * d; break; }
-                    off -= p.rows;
-                }
-                HIPCHK(c, hipMemcpy(row.data(), src, d * sizeof(float), hipMemcpyDeviceToHost));
-                const int nw = empty[t], old = (int)labels[f];
-                for (int e = 0; e < d; e++) sums[(size_t)old * d + e] -= (double)row[e];
-                counts[old] -= 1;
-                for (int e = 0; e < d; e++) sums[(size_t)nw * d + e] = (double)row[e];
-                counts[nw] = 1;
-            }
-        }
-    }
-    std::vector<float> Cn((size_t)k * d);
-    int big = 0;
-    for (int j = 1; j < k; j++)
-        if (counts[j] > counts[big]) big = j;
-    for (int j = 0; j < k; j++)
-        if (counts[j] > 0)
-            for (int e = 0; e < d; e++) Cn[(size_t)j * d + e] = (float)(sums[(size_t)j * d + e] / (double)counts[j]);
-    for (int j = 0; j < k; j++)
-        if (counts[j] <= 0)
-            for (int e = 0; e < d; e++) Cn[(size_t)j * d + e] = Cn[(size_t)big * d + e];
-    HIPCHK(c, hipMemcpyAsync(c->Cb[(pass + 1) & 1].p, Cn.data(), Cn.size() * sizeof(float), hipMemcpyHostToDevice,
-                             c->stream));
+    HIPCHK(c, launch(c, KK_RELOCATE, [&] {
+        return km_launch_relocate(c->tot.p, k, d, c->n, c->best.p, c->labels.p, px.data(), pr.data(), (int)px.size(),
+                                  c->rl_parts.p, c->rl_st.p, c->rl_empty.p, c->rl_sel.p, c->rl_sel.p + k, c->rl_tie.p,
+                                  c->rl_ws.p, c->Cb[(pass + 1) & 1].p, c->dev.cus, c->stream);
+    }));
+    uint32_t ne = 0;
+    HIPCHK(c, hipMemcpyAsync(&ne, c->rl_st.p + KM_RELOC_NEMPTY_WORD, sizeof ne, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    *n_empty_out = (int)ne;
     return KM_OK;
 }
 

@@ -61,6 +61,7 @@ enum km_kernel_id {
     KK_BIG_RESCORE,
     KK_BIG_ACCUM,
     KK_SEED_PP,
+    KK_RELOCATE,
     KK_COUNT
 };
 extern const char *const km_kernel_names[KK_COUNT];
@@ -176,6 +177,20 @@ hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, i
                                  uint16_t *Cop, float *maxes, km_control *ctl, const int32_t *stop, hipStream_t s);
 // xmax: the largest |x|^2 over every slice (float bits), for the approximate mode's half-precision guard
 hipError_t km_launch_big_xmax(const float *xsq, int64_t n, uint32_t *xmax, hipStream_t s);
+
+// ---- empty-cluster relocation on the device (km_reloc.hip)
+// Words of the selection state; blocks of the tie count (its size).
+size_t km_reloc_state_words();
+int64_t km_reloc_blocks(int64_t n, int cus);
+// From the pass's totals tot (k, d + 2) and every row's label and best: the empty clusters (empties, k), the rows
+// they take (sel, ord: k each), the patched float64 totals (ws, k (d + 2)) and the next centres Cn (k, d).
+// part_X / part_rows: the slices in row order (copied into parts_dev, 16 bytes each). State word 5 holds the
+// number of empty clusters afterwards.
+hipError_t km_launch_relocate(const double *tot, int k, int d, int64_t n, const float *best, const uint32_t *labels,
+                              const float *const *part_X, const int64_t *part_rows, int nparts, void *parts_dev,
+                              uint32_t *st, int32_t *empties, int64_t *sel, int64_t *ord, uint32_t *tiecnt,
+                              double *ws, float *Cn, int cus, hipStream_t s);
+#define KM_RELOC_NEMPTY_WORD 5
 // KM_APPROX approximates from KM_APPROX_MIN_DIMS dims while sqrt(max |x|^2 max |c|^2) < 65504 / 4; exact otherwise
 #define KM_APPROX_MIN_DIMS 64
 hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq,
