@@ -1,4 +1,4 @@
-// Exact Lloyd pass for wide rows (16 < dims <= 768, k <= 4096): the reference's "tiles" design (core.py:616-651,
+// Exact Lloyd pass for wide rows (16 < dims <= 768, k <= 65536): the reference's "tiles" design (core.py:616-651,
 // 310-377: matrix-unit dot products, an error margin, exact rescoring of the candidates) rebuilt for CDNA4, plus
 // its sorted accumulation (core.py:934-994, 424-449, 1421-1441).
 //
@@ -10,17 +10,24 @@
 //                   over the centres: the row's smallest packed key (value, centre index) so far, and the centres
 //                   inside the error window around it - every centre that can hold the exact minimum
 //   k_big_rescore   the rows loop (core.py:263-274) on those candidates only, ascending index, strict '<'
-//   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every centre
+//   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every
+//                   centre, 64 rows x 64 centres per block step
 //   k_big_hist/scan/scatter/segsum   a stable counting sort of the rows by label and per-cluster sums in row
 //                   order (float64), the totals of the pass
 //
 // Labels and best are the rows loop's bit for bit (see the window below). With mode KM_APPROX the screen's
 // minimiser is taken on trust, as the reference's exact=False path does (core.py:878-890, 1061-1088), only its
 // distance is computed exactly.
+//
+// Large k (more than 4096 centres, the regime the reference's cascade pruning serves, core.py:1091-1260): the keys
+// carry no index (PACK = false; no perturbation either), each listed key keeps its centre index beside it in LDS,
+// the counting sort keeps its counters in global memory, and exact=False is served exactly.
 #pragma clang fp contract(off)
 #include "km_internal.h"
 #include "kmeans_hip.h"
 #include <math.h>
+
+#include <algorithm>
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -236,7 +243,7 @@ __global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C
 // window, and at the end keeps the listed centres inside the final window - exactly the centres the final window
 // admits. A half-row with more than KB_HALF of them at once (or non-finite data) sends the row to a full scan.
 
-template <int DS>
+template <int DS, bool PACK>
 __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
@@ -277,7 +284,8 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     bf16x8 Bone;
 #pragma unroll
     for (int q = 0; q < 8; q++) Bone[q] = (__bf16)((h == 0 && q < 2) ? 1.0f : 0.0f);
-    const uint32_t IMASK = (1u << ib) - 1u;
+    const uint32_t IMASK = PACK ? (1u << ib) - 1u : 0u;
+    if (!PACK) approx = 0;
 
     // A operand slices: chunk ch is SPC slices of SLK K-steps (the last possibly shorter), staged through a
     // two-slice LDS ring; slice g is loaded while slice g - 1 is multiplied.
@@ -341,6 +349,10 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     // against the current bound, and if still full the row takes the full scan). Approximate mode keeps only the
     // smallest key.
     float *list = reinterpret_cast<float *>(ring + 2 * SLK * 1024) + (size_t)wave * KB_HALF * 64 + lane;
+    // without packed keys, the listed keys' centre indices (after the KB_WAVES lists of keys)
+    uint16_t *lidx = reinterpret_cast<uint16_t *>(reinterpret_cast<float *>(ring + 2 * SLK * 1024) +
+                                                  (size_t)KB_WAVES * KB_HALF * 64) +
+                     (size_t)wave * KB_HALF * 64 + lane;
     issue(0);
     float m1 = 3.4e38f;
     int cnt = 0;
@@ -352,8 +364,11 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
-            key[v] = kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx);
-            m1 = kb_min(m1, key[v]);
+            key[v] = PACK ? kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx) : acc[v];
+            // Without packing, key[v] is the matrix cores' result register itself: the first instruction to
+            // read it must be compiled code, whose hazard tracking inserts the wait states an MFMA result needs
+            // (inline assembly here read stale accumulators)
+            m1 = PACK ? kb_min(m1, key[v]) : fminf(m1, key[v]);
         }
         if (approx) continue;
         const float mrow = kb_min(m1, kb_partner(m1, lane));
@@ -372,12 +387,18 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
                         int w = 0;
                         for (int q = 0; q < KB_HALF; q++) {
                             const float kq = list[q * 64];
-                            if (kq <= Tp) list[(w++) * 64] = kq;
+                            if (kq <= Tp) {
+                                if (!PACK) lidx[w * 64] = lidx[q * 64];
+                                list[(w++) * 64] = kq;
+                            }
                         }
                         cnt = w;
                         spill = cnt == KB_HALF;
                     }
-                    if (cnt < KB_HALF) list[(cnt++) * 64] = key[v];
+                    if (cnt < KB_HALF) {
+                        if (!PACK) lidx[cnt * 64] = (uint16_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
+                        list[(cnt++) * 64] = key[v];
+                    }
                 }
             }
         }
@@ -390,7 +411,8 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
         int w = 0;
         for (int q = 0; q < cnt; q++) {
             const float kq = list[q * 64];
-            if (kq <= Tp) cand[row * KB_CAP + h * KB_HALF + (w++)] = (uint16_t)(kb_u32(kq) & IMASK);
+            if (kq <= Tp)
+                cand[row * KB_CAP + h * KB_HALF + (w++)] = PACK ? (uint16_t)(kb_u32(kq) & IMASK) : lidx[q * 64];
         }
         cnt = w;
     }
@@ -620,65 +642,103 @@ __global__ __launch_bounds__(256) void k_big_label1(const uint16_t *__restrict__
 // 32 dims per chunk (coalesced), thread t carrying the direct-form sum of centre c0 + t; each thread keeps its
 // smallest value over its centres (ascending, strict '<'), then the block keeps the smallest value, lowest index
 // among equal values - the rows loop's label and best.
+// Rows the screen could not narrow (more than KB_HALF window centres in a half-row, or non-finite data) take the
+// rows loop over every centre. Blocks of 256 threads take 64 listed rows at a time against chunks of 64 centres:
+// 32 dims of the rows and of the centres staged in LDS per step, each thread carrying 4 rows x 4 centres of
+// direct-form sums (dims ascending, product and add rounded separately) across the steps, then keeping per row
+// the smallest distance with a strict '<' over its centres in ascending order. The 16 threads that share a row
+// then reduce (value, index) with the lowest index on ties: the rows loop's label and best, label 0 and best +inf
+// included when no distance compares below +inf.
+static constexpr int KB_FR = 64;      // rows per full-scan tile
+static constexpr int KB_FC = 64;      // centres per full-scan chunk
 __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ X, int d, const float *__restrict__ C,
                                                       int k, const uint32_t *__restrict__ over,
                                                       km_control *__restrict__ ctl, uint32_t *__restrict__ labels,
                                                       float *__restrict__ best, const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
-    extern __shared__ float xrow[];
-    __shared__ float cs[256 * (KB_RCH + 1)];
-    __shared__ float sb[256];
-    __shared__ uint32_t sl[256];
+    __shared__ float xs[KB_RCH][KB_FR + 1];   // [dim][row]
+    __shared__ float cs[KB_RCH][KB_FC + 1];   // [dim][centre]
+    __shared__ int64_t rows[KB_FR];
     const int tid = threadIdx.x;
+    const int tr = tid >> 4, tc = tid & 15;   // rows 4 tr .. 4 tr + 3, centres 4 tc .. 4 tc + 3 of a chunk
     const uint32_t total = ctl->n_over;
     if (blockIdx.x == 0 && tid == 0) atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)total);
-    for (uint32_t q = blockIdx.x; q < total; q += gridDim.x) {
-        const int64_t row = over[q];
+    for (uint32_t t0 = blockIdx.x * KB_FR; t0 < total; t0 += gridDim.x * KB_FR) {
+        const int nr = (int)((total - t0) < (uint32_t)KB_FR ? (total - t0) : (uint32_t)KB_FR);
+        __syncthreads();   // the previous tile's rows are no longer read
+        if (tid < KB_FR) rows[tid] = tid < nr ? (int64_t)over[t0 + tid] : (int64_t)over[t0];
         __syncthreads();
-        for (int j = tid; j < d; j += 256) xrow[j] = X[row * d + j];
-        float bst = INFINITY;
-        uint32_t bl = 0;
-        for (int c0 = 0; c0 < k; c0 += 256) {
-            const int nc = (k - c0) < 256 ? (k - c0) : 256;
-            float sacc = 0.0f;
+        float bst[4];
+        uint32_t bl[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            bst[a] = INFINITY;
+            bl[a] = 0u;
+        }
+        for (int c0 = 0; c0 < k; c0 += KB_FC) {
+            float sacc[4][4];
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) sacc[a][b] = 0.0f;
             for (int j0 = 0; j0 < d; j0 += KB_RCH) {
                 const int w = (d - j0) < KB_RCH ? (d - j0) : KB_RCH;
                 __syncthreads();
-                for (int e = tid; e < nc * KB_RCH; e += 256) {
-                    const int i = e / KB_RCH, jj = e - (e / KB_RCH) * KB_RCH;
-                    cs[i * (KB_RCH + 1) + jj] = jj < w ? C[(int64_t)(c0 + i) * d + j0 + jj] : 0.0f;
+                for (int e = tid; e < KB_FR * KB_RCH; e += 256) {
+                    const int r = e / KB_RCH, jj = e - (e / KB_RCH) * KB_RCH;
+                    xs[jj][r] = jj < w ? X[rows[r] * d + j0 + jj] : 0.0f;
+                }
+                for (int e = tid; e < KB_FC * KB_RCH; e += 256) {
+                    const int c = e / KB_RCH, jj = e - (e / KB_RCH) * KB_RCH;
+                    cs[jj][c] = (jj < w && c0 + c < k) ? C[(int64_t)(c0 + c) * d + j0 + jj] : 0.0f;
                 }
                 __syncthreads();
-                if (tid < nc) {
-                    const float *cc = cs + tid * (KB_RCH + 1);
-                    float sv = sacc;
-                    for (int jj = 0; jj < w; jj++) {
-                        const float t = xrow[j0 + jj] - cc[jj];
-                        sv = sv + t * t;
-                    }
-                    sacc = sv;
+                for (int jj = 0; jj < w; jj++) {
+                    float xv[4], cv[4];
+#pragma unroll
+                    for (int a = 0; a < 4; a++) xv[a] = xs[jj][4 * tr + a];
+#pragma unroll
+                    for (int b = 0; b < 4; b++) cv[b] = cs[jj][4 * tc + b];
+#pragma unroll
+                    for (int a = 0; a < 4; a++)
+#pragma unroll
+                        for (int b = 0; b < 4; b++) {
+                            const float t = xv[a] - cv[b];
+                            sacc[a][b] = sacc[a][b] + t * t;
+                        }
                 }
             }
-            if (tid < nc && sacc < bst) { bst = sacc; bl = (uint32_t)(c0 + tid); }
-        }
-        __syncthreads();
-        sb[tid] = bst;
-        sl[tid] = bl;
-        __syncthreads();
-        for (int hh = 128; hh > 0; hh >>= 1) {
-            if (tid < hh) {
-                const float ob = sb[tid + hh];
-                const uint32_t ol = sl[tid + hh];
-                if (ob < sb[tid] || (ob == sb[tid] && ol < sl[tid])) {
-                    sb[tid] = ob;
-                    sl[tid] = ol;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int c = c0 + 4 * tc + b;
+                if (c < k) {
+#pragma unroll
+                    for (int a = 0; a < 4; a++)
+                        if (sacc[a][b] < bst[a]) {
+                            bst[a] = sacc[a][b];
+                            bl[a] = (uint32_t)c;
+                        }
                 }
             }
-            __syncthreads();
         }
-        if (tid == 0) {
-            labels[row] = sl[0];
-            best[row] = sb[0];
+        // the 16 threads of a row group (consecutive lanes of one wave): smallest value, lowest index on ties
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            float v = bst[a];
+            uint32_t ix = bl[a];
+            for (int off = 8; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(v, off);
+                const uint32_t oi = (uint32_t)__shfl_xor((int)ix, off);
+                if (ov < v || (ov == v && oi < ix)) {
+                    v = ov;
+                    ix = oi;
+                }
+            }
+            const int r = 4 * tr + a;
+            if (tc == 0 && r < nr) {
+                labels[rows[r]] = ix;
+                best[rows[r]] = v;
+            }
         }
     }
 }
@@ -705,6 +765,20 @@ __global__ __launch_bounds__(256) void k_big_hist(const uint32_t *__restrict__ l
     for (int64_t r = r0 + threadIdx.x; r < r1; r += 256) atomicAdd(&cnt[labels[r]], 1u);
     __syncthreads();
     for (int c = threadIdx.x; c < k; c += 256) H[(int64_t)blockIdx.x * k + c] = cnt[c];
+}
+
+// The same histogram with the counters in global memory (H zeroed first), for k too large for LDS.
+__global__ __launch_bounds__(256) void k_big_hist_g(const uint32_t *__restrict__ labels, int64_t n, int k,
+                                                    uint32_t *__restrict__ H, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
+    const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
+    for (int64_t r = r0 + threadIdx.x; r < r1; r += 256) atomicAdd(&H[(int64_t)blockIdx.x * k + labels[r]], 1u);
+}
+
+__global__ __launch_bounds__(256) void k_big_zero(uint32_t *__restrict__ p, int64_t n, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) p[e] = 0u;
 }
 
 // One block: O[b][c] = (rows with label < c) + (rows with label c in blocks before b); counts[c] = its total.
@@ -780,6 +854,36 @@ __global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict_
         if (valid) perm[run[L] + before] = (uint32_t)r;
         __syncthreads();
         if (valid && after == 0) run[L] += before + 1;   // the last row of each label advances its offset
+    }
+}
+
+// k_big_scatter with the running offsets in global memory: this block's row of O (O[b][c] + base[c] is the
+// next place of label c; the last row of each label in a round of 256 advances it).
+__global__ __launch_bounds__(256) void k_big_scatter_g(const uint32_t *__restrict__ labels, int64_t n, int k,
+                                                       uint32_t *__restrict__ O, const uint32_t *__restrict__ base,
+                                                       uint32_t *__restrict__ perm, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    __shared__ uint32_t lab[256];
+    uint32_t *run = O + (int64_t)blockIdx.x * k;
+    const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
+    const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
+    for (int64_t q = r0; q < r1; q += 256) {
+        const int64_t r = q + threadIdx.x;
+        const bool valid = r < r1;
+        const uint32_t L = valid ? labels[r] : 0xffffffffu;
+        __syncthreads();   // the previous round's offsets are written, its labels read
+        lab[threadIdx.x] = L;
+        __syncthreads();
+        uint32_t before = 0, after = 0;
+        for (int t = 0; t < 256; t++) {
+            const uint32_t o = lab[t];
+            before += (t < (int)threadIdx.x && o == L) ? 1u : 0u;
+            after += (t > (int)threadIdx.x && o == L) ? 1u : 0u;
+        }
+        const uint32_t at = valid ? run[L] : 0u;
+        if (valid) perm[base[L] + at + before] = (uint32_t)r;
+        __syncthreads();   // every thread has read its label's offset before the last row advances it
+        if (valid && after == 0) run[L] = at + before + 1;
     }
 }
 
@@ -883,15 +987,16 @@ typedef void (*screen_fn)(const uint16_t *, const float *, int64_t, int, const u
                           int, float, int, const uint32_t *, uint16_t *, uint16_t *, uint32_t *, uint32_t *,
                           km_control *, const int32_t *);
 
+template <bool PACK>
 static screen_fn kb_screen_for(int DS) {
     switch (DS) {
-        case 2: return k_big_screen<2>;
-        case 4: return k_big_screen<4>;
-        case 8: return k_big_screen<8>;
-        case 16: return k_big_screen<16>;
-        case 24: return k_big_screen<24>;
-        case 32: return k_big_screen<32>;
-        case 48: return k_big_screen<48>;
+        case 2: return k_big_screen<2, PACK>;
+        case 4: return k_big_screen<4, PACK>;
+        case 8: return k_big_screen<8, PACK>;
+        case 16: return k_big_screen<16, PACK>;
+        case 24: return k_big_screen<24, PACK>;
+        case 32: return k_big_screen<32, PACK>;
+        case 48: return k_big_screen<48, PACK>;
         default: return nullptr;
     }
 }
@@ -906,7 +1011,7 @@ static int kb_ds(int d) {
 
 km_big_plan km_plan_big(int64_t n, int d, int k) {
     km_big_plan pl{};
-    if (d <= 16 || d > 768 || k < 1 || k > 4096 || n < 1) return pl;
+    if (d <= 16 || d > 768 || k < 1 || k > KM_BIG_MAX_K || n < 1) return pl;
     pl.ok = 1;
     pl.DS = kb_ds(d);
     pl.kpad = (k + 31) / 32 * 32;
@@ -914,7 +1019,7 @@ km_big_plan km_plan_big(int64_t n, int d, int k) {
     int ib = 0;
     while ((1 << ib) < pl.kpad) ib++;
     if (ib < 1) ib = 1;
-    pl.ib = ib;
+    pl.ib = k <= KM_BIG_PACK_MAX_K ? ib : 0;
     pl.ntiles = (n + 31) / 32;
     pl.nb = (int)((n + KB_RB - 1) / KB_RB);
     return pl;
@@ -956,14 +1061,16 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
                                 const uint32_t *xmax, int64_t n, int d, const uint16_t *Cop, const float *maxes, int k,
                                 uint16_t *ncand, uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
                                 const int32_t *stop, hipStream_t s) {
-    screen_fn fn = kb_screen_for(pl.DS);
+    const bool pack = pl.ib > 0;
+    screen_fn fn = pack ? kb_screen_for<true>(pl.DS) : kb_screen_for<false>(pl.DS);
     if (!fn) return hipErrorInvalidValue;
-    const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
+    const float rho = pack ? (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23) : 0.0f;
     const unsigned blocks = (unsigned)((pl.ntiles + KB_WAVES - 1) / KB_WAVES);
     // exact=False approximates from 64 dims, and only under the half-precision guard (checked in the kernel);
     // below 64 dims the reference's dispatch runs its exact kernels (core.py:2036-2042)
     const int approx = (mode == KM_APPROX && d >= KM_APPROX_MIN_DIMS) ? 1 : 0;
-    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), 2 * KB_SLICE * 1024 + KB_WAVES * KB_HALF * 64 * 4, s, X16T,
+    const size_t lds = 2 * KB_SLICE * 1024 + KB_WAVES * KB_HALF * 64 * (pack ? 4 : 6);
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), lds, s, X16T,
                        xsq, n, d, Cop, maxes, k, pl.nchunks, pl.ib, rho, approx, xmax, ncand, cand, over, multi, ctl,
                        stop);
     return hipGetLastError();
@@ -990,7 +1097,7 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
                            ctl, labels, best, stop);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), (size_t)d * 4, s, X, d, C, k, over, ctl, labels, best,
+    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, ctl, labels, best,
                        stop);
     return hipGetLastError();
 }
@@ -998,13 +1105,26 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
                                uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
-    hipLaunchKernelGGL(k_big_hist, dim3(pl.nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    // counters in LDS up to KM_BIG_PACK_MAX_K labels (16 KB), in global memory above
+    const bool glob = k > KM_BIG_PACK_MAX_K;
+    hipError_t e;
+    if (glob) {
+        const int64_t cells = (int64_t)pl.nb * k;
+        hipLaunchKernelGGL(k_big_zero, dim3((unsigned)std::min<int64_t>((cells + 255) / 256, 4096)), dim3(256), 0, s, H,
+                           cells, stop);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_big_hist_g, dim3(pl.nb), dim3(256), 0, s, labels, n, k, H, stop);
+    } else {
+        hipLaunchKernelGGL(k_big_hist, dim3(pl.nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_big_scan, dim3(1), dim3(1024), 0, s, H, pl.nb, k, counts, base, stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_scatter, dim3(pl.nb), dim3(256), (size_t)(k + 256) * 4, s, labels, n, k, H, base, perm,
-                       stop);
+    if (glob)
+        hipLaunchKernelGGL(k_big_scatter_g, dim3(pl.nb), dim3(256), 0, s, labels, n, k, H, base, perm, stop);
+    else
+        hipLaunchKernelGGL(k_big_scatter, dim3(pl.nb), dim3(256), (size_t)(k + 256) * 4, s, labels, n, k, H, base,
+                           perm, stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(C_lite ? k_big_segsum<true> : k_big_segsum<false>, dim3(k), dim3(64 * KB_SEGW),
                        (size_t)KB_SEGW * (d + 1) * 8, s, X, d, best, C_lite, perm, (int64_t)0, counts, base, k, tmp,

@@ -164,10 +164,14 @@ struct km_big_plan {
     int DS;          // MFMA K-steps over the padded dims (16 DS >= dims)
     int kpad;        // centres padded to a multiple of 32
     int nchunks;     // kpad / 32
-    int ib;          // centre-index bits packed into keys
+    int ib;          // centre-index bits packed into keys (0: keys carry no index, k > KM_BIG_PACK_MAX_K)
     int64_t ntiles;  // 32-row tiles
     int nb;          // 4096-row blocks of the sort
 };
+// Largest k whose keys carry the centre index in their low mantissa bits (12 bits: a relative perturbation of
+// 2^-11 at most); above it, up to KM_BIG_MAX_K, the screen keeps each listed key's index beside it.
+#define KM_BIG_PACK_MAX_K 4096
+#define KM_BIG_MAX_K 65536   // centre indices are uint16 (0 .. 65535)
 km_big_plan km_plan_big(int64_t n, int d, int k);
 size_t km_big_x16_elems(const km_big_plan &pl);   // uint16 elements of the bf16 row operands
 size_t km_big_cop_elems(const km_big_plan &pl);   // uint16 elements of the bf16 centre operands
