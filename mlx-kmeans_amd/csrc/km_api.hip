@@ -560,7 +560,37 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         return finish_pass(c, k, rb, pass, tol, flags, stop);
     }
 
-    // rows path: exact labels for every slice, then the generic accumulation
+    // rows path: exact labels for every slice, then the generic accumulation (or, at large k, the counting sort)
+    if (k > KM_SORTED_MIN_K) {
+        const int64_t kw = (int64_t)k * (d + 2);
+        int64_t max_rows = 0;
+        for (auto &p : c->parts) max_rows = std::max(max_rows, p.rows);
+        HIPCHK(c, c->labels.ensure((size_t)c->n));
+        HIPCHK(c, c->best.ensure((size_t)c->n));
+        HIPCHK(c, c->hist.ensure((size_t)km_sorted_blocks(max_rows) * k));
+        HIPCHK(c, c->counts.ensure((size_t)k));
+        HIPCHK(c, c->base.ensure((size_t)k));
+        HIPCHK(c, c->perm.ensure((size_t)max_rows));
+        HIPCHK(c, c->tot.ensure((size_t)kw));
+        const int S = (int)c->parts.size();
+        HIPCHK(c, c->red.ensure((size_t)S * kw));
+        uint32_t *lab_all = labels_d ? labels_d : c->labels.p;
+        float *best_all = best_d ? best_d : c->best.p;
+        int64_t row0 = 0;
+        for (size_t i = 0; i < c->parts.size(); i++) {
+            const Part &p = c->parts[i];
+            HIPCHK(c, launch(c, KK_ASSIGN_ROWS, [&] {
+                return km_launch_assign_rows(p.X, p.rows, d, Cin, k, lab_all + row0, best_all + row0, stop, c->stream);
+            }));
+            HIPCHK(c, launch(c, KK_ACCUM_GENERIC, [&] {
+                return km_launch_sorted_accum(p.X, p.rows, d, lab_all + row0, best_all + row0, k, c->hist.p,
+                                              c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw, stop,
+                                              c->stream);
+            }));
+            row0 += p.rows;
+        }
+        return finish_pass(c, k, 0, pass, tol, flags, stop, S);
+    }
     size_t total_rb = 0;
     std::vector<km_accum_plan> plans;
     for (auto &p : c->parts) {

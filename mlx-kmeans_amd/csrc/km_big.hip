@@ -1102,6 +1102,17 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
     return hipGetLastError();
 }
 
+int64_t km_sorted_blocks(int64_t n) { return (n + KB_RB - 1) / KB_RB; }
+
+hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32_t *labels, const float *best, int k,
+                                  uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *tmp,
+                                  const int32_t *stop, hipStream_t s) {
+    if (d < 1 || d > 64 * 13 - 1) return hipErrorInvalidValue;
+    km_big_plan pl{};
+    pl.nb = (int)km_sorted_blocks(n);
+    return km_launch_big_accum(pl, X, n, d, labels, best, nullptr, k, H, counts, base, perm, tmp, stop, s);
+}
+
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
                                uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {

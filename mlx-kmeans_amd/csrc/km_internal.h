@@ -209,3 +209,12 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
                                uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s);
+// The counting sort by label and per-cluster float64 sums in row order for any rows path (d < 832): rows whose
+// labels and best are known. H holds km_sorted_blocks(n) x k counters; tmp receives the k (d + 2) range sums.
+int64_t km_sorted_blocks(int64_t n);
+hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32_t *labels, const float *best, int k,
+                                  uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *tmp,
+                                  const int32_t *stop, hipStream_t s);
+// Centres above which the rows path accumulates through the counting sort (the generic accumulation re-reads the
+// rows once per block of clusters)
+#define KM_SORTED_MIN_K 4096
