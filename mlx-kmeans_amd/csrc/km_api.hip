@@ -96,6 +96,18 @@ struct km_ctx {
     DBuf<double> rl_ws;             // relocation: the patched totals
     DBuf<char> rl_parts;            // relocation: the slice table
     DBuf<char> pp_ws;           // k-means++: the rounds' workspace
+    // change-only accumulation of the wide-row fit loop: labels alternate between `labels` (even passes) and
+    // wlab (odd passes), each pass compared with the other
+    DBuf<uint32_t> wlab;
+    DBuf<uint32_t> wd_bcnt, wd_e;   // per-block change counts + m; the entry arrays (elab, erow: wd_limit each x2)
+    DBuf<uint32_t> wd_H, wd_cnt, wd_base, wd_perm;   // the entries' counting sort by label (k + 1 labels)
+    DBuf<int32_t> wd_gate;          // [0] nonzero: no change-only sums this pass; [1] nonzero: no full accumulation
+    DBuf<double> wd_part, wd_mu;    // mean / scatter partials; [mu (d), T] of the data set
+    DBuf<double> wd_pieces;         // the change sums of clusters that span several chunks, per chunk
+    DBuf<km_slice> wd_slices;       // the slice table on the device
+    std::vector<km_slice> wd_slices_h;
+    bool wd_ready = false;          // wd_mu and wd_slices describe the current data
+    int64_t wd_limit = 0;           // the most changed rows a change-only pass takes
     km_control *ctl = nullptr;    // device
     km_control *ctl_h = nullptr;  // pinned host mirror
     unsigned char *scratch = nullptr;   // device address of this device's copy of `scratch` (km_pass_noalloc)
@@ -212,6 +224,7 @@ static void drop_parts(km_ctx *c) {
     c->parts.clear();
     c->n = 0;
     c->d = 0;
+    c->wd_ready = false;
 }
 
 extern "C" void km_destroy(km_ctx *c) {
@@ -246,6 +259,18 @@ extern "C" void km_destroy(km_ctx *c) {
     c->pp_C.release();
     c->pp_idx.release();
     c->pp_ws.release();
+    c->wlab.release();
+    c->wd_bcnt.release();
+    c->wd_e.release();
+    c->wd_H.release();
+    c->wd_cnt.release();
+    c->wd_base.release();
+    c->wd_perm.release();
+    c->wd_pieces.release();
+    c->wd_gate.release();
+    c->wd_part.release();
+    c->wd_mu.release();
+    c->wd_slices.release();
     c->rl_st.release();
     c->rl_tie.release();
     c->rl_empty.release();
@@ -291,6 +316,7 @@ static int add_part(km_ctx *c, const float *X, int64_t rows, int32_t where) {
     }
     c->parts.push_back(p);
     c->n += rows;
+    c->wd_ready = false;
     return KM_OK;
 }
 
@@ -387,7 +413,7 @@ static int ensure_pass_buffers(km_ctx *c, int k, size_t total_rb, bool need_rows
 // Partials -> totals in c->tot, and with KM_FIN_UPDATE the new centres into Cb[(pass + 1) & 1] and the pass
 // statistics into the control block. presummed > 0: c->red already holds that many range sums.
 static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags, const int32_t *stop,
-                       int presummed = 0) {
+                       int presummed = 0, const int32_t *dsel = nullptr) {
     const int d = c->d;
     const int64_t kw = (int64_t)k * (d + 2);
     float *Cn = c->Cb[(pass + 1) & 1].p;
@@ -399,14 +425,19 @@ static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags
         }));
         return KM_OK;
     }
-    HIPCHK(c, launch(c, KK_FINISH, [&] { return km_launch_finish(c->red.p, presummed, k, d, c->tot.p, Cn, c->ctl, pass, tol, flags, stop, c->stream); }));
+    HIPCHK(c, launch(c, KK_FINISH, [&] {
+        return km_launch_finish(c->red.p, presummed, k, d, c->tot.p, Cn, c->ctl, pass, tol, flags, stop, c->stream,
+                                dsel ? c->Cb[pass & 1].p : nullptr, dsel ? c->wd_mu.p : nullptr, dsel);
+    }));
     return KM_OK;
 }
 
 // The wide-row pass: centre operands, then per slice the screen + exact rescoring (labels and best for every
-// row) and the sorted accumulation into one range sum per slice, then the finish.
+// row), then per slice the sorted accumulation into one range sum per slice, then the finish. In the fit loop
+// (lmode set) the labels alternate between two arrays by pass parity; a KM_LSTATE_DELTA pass counts the rows that
+// changed since the previous pass and, when few did, accumulates only those (the full accumulation stands down).
 static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d, const int32_t *stop, int pass,
-                   double tol, int flags) {
+                   double tol, int flags, int lmode) {
     const int d = c->d;
     const int64_t kw = (int64_t)k * (d + 2);
     const float *Cin = c->Cb[pass & 1].p;
@@ -453,7 +484,11 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, c->tot.ensure((size_t)kw));
     const int S = (int)c->parts.size();
     HIPCHK(c, c->red.ensure((size_t)S * kw));
-    uint32_t *lab_all = labels_d ? labels_d : c->labels.p;
+    const bool wd = lmode != KM_LSTATE_NONE && !labels_d && !best_d;
+    const bool delta = wd && lmode == KM_LSTATE_DELTA;
+    if (wd) HIPCHK(c, c->wlab.ensure((size_t)c->n));
+    uint32_t *lab_all = labels_d ? labels_d : (wd && (pass & 1)) ? c->wlab.p : c->labels.p;
+    const uint32_t *lab_prev = (pass & 1) ? c->labels.p : c->wlab.p;
     float *best_all = best_d ? best_d : c->best.p;
     // without per-row outputs, single-candidate rows skip the rescoring and the accumulation adds the distances
     const int lite = (labels_d || best_d) ? 0 : 1;
@@ -477,14 +512,33 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
             return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->multi.p,
                                          c->ctl, lab_all + row0, best_all + row0, lite, stop, c->stream);
         }));
+        row0 += p.rows;
+    }
+    const int32_t *full_gate = stop;
+    if (delta) {   // the gate: the change-only sums or the full accumulation, chosen on the device
+        HIPCHK(c, launch(c, KK_CHANGE, [&] {
+            return km_launch_wd_gate(lab_all, lab_prev, c->n, c->wd_limit, c->wd_bcnt.p, c->wd_gate.p, stop, c->stream);
+        }));
+        full_gate = c->wd_gate.p + 1;
+    }
+    row0 = 0;
+    for (size_t i = 0; i < c->parts.size(); i++) {
+        const Part &p = c->parts[i];
+        const km_big_plan bp = km_plan_big(p.rows, d, k);
         HIPCHK(c, launch(c, KK_BIG_ACCUM, [&] {
             return km_launch_big_accum(bp, p.X, p.rows, d, lab_all + row0, best_all + row0, lite ? Cin : nullptr, k,
-                                       c->hist.p, c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw, stop,
-                                       c->stream);
+                                       c->hist.p, c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw,
+                                       full_gate, c->stream);
         }));
         row0 += p.rows;
     }
-    return finish_pass(c, k, 0, pass, tol, flags, stop, S);
+    if (!delta) return finish_pass(c, k, 0, pass, tol, flags, stop, S);
+    HIPCHK(c, launch(c, KK_CHANGE, [&] {
+        return km_launch_wd_accum(c->wd_slices.p, (int)c->parts.size(), c->n, d, lab_all, lab_prev, k, c->wd_limit,
+                                  c->wd_bcnt.p, c->wd_e.p, c->wd_e.p + 2 * c->wd_limit, c->wd_H.p, c->wd_cnt.p,
+                                  c->wd_base.p, c->wd_perm.p, c->wd_pieces.p, c->red.p, c->wd_gate.p, c->stream);
+    }));
+    return finish_pass(c, k, 0, pass, tol, flags, stop, S, c->wd_gate.p);
 }
 
 // Pass `pass`: assignment + accumulation over every slice with the centres in Cb[pass & 1], then the finish
@@ -504,7 +558,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
     const int32_t *stop = gated ? &c->ctl->stop : nullptr;
     const int d = c->d;
 
-    if (fam == FAM_BIG) return run_big(c, k, mode, labels_d, best_d, stop, pass, tol, flags);
+    if (fam == FAM_BIG) return run_big(c, k, mode, labels_d, best_d, stop, pass, tol, flags, lmode);
 
     if (fam == FAM_MFMA_FUSED) {
         // without per-row outputs the kernel skips the direct form for rows the screen settles alone
@@ -759,12 +813,63 @@ static int queue_iteration(km_ctx *c, int k, int mode, int path, int pass, doubl
                     KM_FIN_UPDATE | (spherical ? KM_FIN_SPHERICAL : 0), lmode);
 }
 
-// The fit loop keeps every row's label between passes where the fused MFMA path runs, so that a pass accumulates
-// only the rows whose label changed. Sizes the label array (each slice's at a 64-row-aligned offset, 64 bytes of
-// padding after it). Returns whether the loop uses it.
+// The most changed rows a pass of the wide-row path takes as change-only sums: they sort 2 limit entries and read
+// each changed row twice, the full accumulation sorts and reads every row once; a quarter of the rows leaves the
+// change-only sums the cheaper at every shape.
+static int64_t wide_delta_limit(int64_t n) { return n / 4; }
+
+// The wide-row path's change-only accumulation: the second label array, the count and entry arrays, and once per
+// data set the slice table and [mu, T] (queued on the stream before the loop's first pass).
+static int prepare_wide_delta(km_ctx *c, int k, bool *use) {
+    *use = false;
+    const int d = c->d;
+    if (d > km_wd_max_dims() || c->n > (int64_t)0x7fffffff) return KM_OK;
+    const int64_t limit = wide_delta_limit(c->n);
+    if (limit < 1) return KM_OK;
+    c->wd_limit = limit;
+    HIPCHK(c, c->labels.ensure((size_t)c->n));
+    HIPCHK(c, c->wlab.ensure((size_t)c->n));
+    HIPCHK(c, c->wd_bcnt.ensure((size_t)km_wd_blocks(c->n) + 1));
+    HIPCHK(c, c->wd_e.ensure((size_t)limit * 4));
+    HIPCHK(c, c->wd_H.ensure((size_t)km_sorted_blocks(2 * limit) * (k + 1)));
+    HIPCHK(c, c->wd_cnt.ensure((size_t)k + 1));
+    HIPCHK(c, c->wd_base.ensure((size_t)k + 1));
+    HIPCHK(c, c->wd_perm.ensure((size_t)limit * 2));
+    HIPCHK(c, c->wd_pieces.ensure((size_t)km_wd_piece_doubles(limit, d)));
+    HIPCHK(c, c->wd_gate.ensure(2));
+    if (!c->wd_ready) {
+        std::vector<int64_t> rows;
+        int64_t nb = 0, row0 = 0;
+        c->wd_slices_h.clear();
+        for (auto &p : c->parts) {
+            c->wd_slices_h.push_back({p.X, row0});
+            rows.push_back(p.rows);
+            nb += km_wd_stat_blocks(p.rows);
+            row0 += p.rows;
+        }
+        HIPCHK(c, c->wd_part.ensure((size_t)nb * (d + 1)));
+        HIPCHK(c, c->wd_mu.ensure((size_t)d + 1));
+        HIPCHK(c, c->wd_slices.ensure(c->wd_slices_h.size()));
+        HIPCHK(c, hipMemcpyAsync(c->wd_slices.p, c->wd_slices_h.data(), c->wd_slices_h.size() * sizeof(km_slice),
+                                 hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, launch(c, KK_BIG_PREP, [&] {
+            return km_launch_wd_stats(c->wd_slices_h.data(), rows.data(), (int)rows.size(), d, c->wd_part.p,
+                                      c->wd_mu.p, c->stream);
+        }));
+        c->wd_ready = true;
+    }
+    *use = true;
+    return KM_OK;
+}
+
+// The fit loop keeps every row's label between passes where the fused MFMA path or the wide-row path runs, so
+// that a pass accumulates only the rows whose label changed. For the fused MFMA path: sizes the label array (each
+// slice's at a 64-row-aligned offset, 64 bytes of padding after it). Returns whether the loop uses it.
 static int prepare_label_state(km_ctx *c, int k, bool *use) {
     km_mfma_plan mp;
-    *use = choose_path(c, k, KM_PATH_AUTO, &mp) == FAM_MFMA_FUSED && k <= 256;
+    const int fam = choose_path(c, k, KM_PATH_AUTO, &mp);
+    if (fam == FAM_BIG) return prepare_wide_delta(c, k, use);
+    *use = fam == FAM_MFMA_FUSED && k <= 256;
     if (!*use) return KM_OK;
     c->lstate_off.clear();
     int64_t off = 0;

@@ -827,64 +827,66 @@ __global__ __launch_bounds__(1024) void k_big_scan(uint32_t *__restrict__ H, int
     }
 }
 
-// Block per 4096 rows, 256 at a time: a row's place is base[label] + O[b][label] + (rows of its label earlier
-// in this block).
-__global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict__ labels, int64_t n, int k,
-                                                     const uint32_t *__restrict__ O, const uint32_t *__restrict__ base,
-                                                     uint32_t *__restrict__ perm, const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    extern __shared__ uint32_t run[];   // k running offsets, then 256 labels
-    uint32_t *lab = run + k;
-    for (int c = threadIdx.x; c < k; c += 256) run[c] = base[c] + O[(int64_t)blockIdx.x * k + c];
+// The lanes of this wave holding the same label as this lane (valid lanes only): one ballot per label bit.
+__device__ __forceinline__ uint64_t kb_peers(uint32_t L, int nbits, bool valid) {
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nbits; b++) {
+        const bool bit = (L >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        peers &= bit ? bal : ~bal;
+    }
+    return peers;
+}
+
+// Block per 4096 rows, 256 at a time: a row's place is base[label] + O[b][label] + (rows of its label earlier in
+// this block). Within a round of 256, a row's rank among its wave's rows of the same label comes from the peer
+// mask; the four waves then take their places in wave order (a barrier between them), the last row of each label
+// in a wave advancing that label's running offset.
+template <bool GLOBAL_RUN>
+__device__ __forceinline__ void kb_scatter_body(const uint32_t *__restrict__ labels, int64_t n, int nbits,
+                                                uint32_t *__restrict__ run, const uint32_t *__restrict__ base,
+                                                uint32_t *__restrict__ perm) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint64_t lt = (1ull << lane) - 1ull;
     const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
     const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
-    for (int64_t q = r0; q < r1; q += 256) {
+    for (int64_t q = r0; q < r1; q += 256) {   // block-uniform trip count: every thread reaches the barriers
         const int64_t r = q + threadIdx.x;
         const bool valid = r < r1;
-        const uint32_t L = valid ? labels[r] : 0xffffffffu;
-        __syncthreads();
-        lab[threadIdx.x] = L;
-        __syncthreads();
-        uint32_t before = 0, after = 0;
-        for (int t = 0; t < 256; t++) {
-            const uint32_t o = lab[t];
-            before += (t < (int)threadIdx.x && o == L) ? 1u : 0u;
-            after += (t > (int)threadIdx.x && o == L) ? 1u : 0u;
+        const uint32_t L = valid ? labels[r] : 0u;
+        const uint64_t peers = kb_peers(L, nbits, valid);
+        const uint32_t rank = (uint32_t)__popcll(peers & lt);
+        const bool last = (peers & ~lt) == (1ull << lane);   // no peer above this lane
+        for (int w = 0; w < 4; w++) {
+            __syncthreads();   // the previous wave's offsets are written
+            if (wave == w && valid) {
+                const uint32_t at = run[L];
+                perm[(GLOBAL_RUN ? base[L] : 0u) + at + rank] = (uint32_t)r;
+                if (last) run[L] = at + rank + 1;
+            }
         }
-        if (valid) perm[run[L] + before] = (uint32_t)r;
-        __syncthreads();
-        if (valid && after == 0) run[L] += before + 1;   // the last row of each label advances its offset
     }
 }
 
-// k_big_scatter with the running offsets in global memory: this block's row of O (O[b][c] + base[c] is the
-// next place of label c; the last row of each label in a round of 256 advances it).
-__global__ __launch_bounds__(256) void k_big_scatter_g(const uint32_t *__restrict__ labels, int64_t n, int k,
-                                                       uint32_t *__restrict__ O, const uint32_t *__restrict__ base,
-                                                       uint32_t *__restrict__ perm, const int32_t *__restrict__ stop) {
+// Running offsets in LDS: run[c] = base[c] + O[b][c].
+__global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict__ labels, int64_t n, int k,
+                                                     int nbits, const uint32_t *__restrict__ O,
+                                                     const uint32_t *__restrict__ base, uint32_t *__restrict__ perm,
+                                                     const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
-    __shared__ uint32_t lab[256];
-    uint32_t *run = O + (int64_t)blockIdx.x * k;
-    const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
-    const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
-    for (int64_t q = r0; q < r1; q += 256) {
-        const int64_t r = q + threadIdx.x;
-        const bool valid = r < r1;
-        const uint32_t L = valid ? labels[r] : 0xffffffffu;
-        __syncthreads();   // the previous round's offsets are written, its labels read
-        lab[threadIdx.x] = L;
-        __syncthreads();
-        uint32_t before = 0, after = 0;
-        for (int t = 0; t < 256; t++) {
-            const uint32_t o = lab[t];
-            before += (t < (int)threadIdx.x && o == L) ? 1u : 0u;
-            after += (t > (int)threadIdx.x && o == L) ? 1u : 0u;
-        }
-        const uint32_t at = valid ? run[L] : 0u;
-        if (valid) perm[base[L] + at + before] = (uint32_t)r;
-        __syncthreads();   // every thread has read its label's offset before the last row advances it
-        if (valid && after == 0) run[L] = at + before + 1;
-    }
+    extern __shared__ uint32_t run[];   // k running offsets
+    for (int c = threadIdx.x; c < k; c += 256) run[c] = base[c] + O[(int64_t)blockIdx.x * k + c];
+    kb_scatter_body<false>(labels, n, nbits, run, base, perm);
+}
+
+// The running offsets in global memory, for k too large for LDS: this block's row of O (O[b][c] + base[c] is the
+// next place of label c).
+__global__ __launch_bounds__(256) void k_big_scatter_g(const uint32_t *__restrict__ labels, int64_t n, int k,
+                                                       int nbits, uint32_t *__restrict__ O,
+                                                       const uint32_t *__restrict__ base, uint32_t *__restrict__ perm,
+                                                       const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    kb_scatter_body<true>(labels, n, nbits, O + (int64_t)blockIdx.x * k, base, perm);
 }
 
 // Block per cluster (KB_SEGW waves, each a fixed consecutive range of the cluster's rows): entries [count, best,
@@ -939,11 +941,16 @@ __global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__rest
             if (q + u < q1) {
                 const int64_t r = r0 + cur[u];
                 const float *x = X + r * d;
+                // unconditional loads (a lane past the last dim reads dim d - 1), masked afterwards: a guarded load
+                // becomes a branch of its own
                 float v[MAXJ];
+#pragma unroll
+                for (int i = 0; i < MAXJ; i++) v[i] = x[min(lane + 64 * i, d - 1)];
+                const float bv = LITE ? 0.0f : best[r];
 #pragma unroll
                 for (int i = 0; i < MAXJ; i++) {
                     const int j = lane + 64 * i;
-                    v[i] = j < d ? x[j] : ((!LITE && j == d) ? best[r] : 0.0f);
+                    if (j >= d) v[i] = (!LITE && j == d) ? bv : 0.0f;
                 }
 #pragma unroll
                 for (int i = 0; i < MAXJ; i++) acc[i] += (double)v[i];
@@ -1113,30 +1120,40 @@ hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32
     return km_launch_big_accum(pl, X, n, d, labels, best, nullptr, k, H, counts, base, perm, tmp, stop, s);
 }
 
-hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
-                               const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
-                               uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
+hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32_t *H, uint32_t *counts,
+                                uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s) {
     // counters in LDS up to KM_BIG_PACK_MAX_K labels (16 KB), in global memory above
     const bool glob = k > KM_BIG_PACK_MAX_K;
+    const int nb = (int)km_sorted_blocks(n);
     hipError_t e;
     if (glob) {
-        const int64_t cells = (int64_t)pl.nb * k;
+        const int64_t cells = (int64_t)nb * k;
         hipLaunchKernelGGL(k_big_zero, dim3((unsigned)std::min<int64_t>((cells + 255) / 256, 4096)), dim3(256), 0, s, H,
                            cells, stop);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(k_big_hist_g, dim3(pl.nb), dim3(256), 0, s, labels, n, k, H, stop);
+        hipLaunchKernelGGL(k_big_hist_g, dim3(nb), dim3(256), 0, s, labels, n, k, H, stop);
     } else {
-        hipLaunchKernelGGL(k_big_hist, dim3(pl.nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
+        hipLaunchKernelGGL(k_big_hist, dim3(nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_scan, dim3(1), dim3(1024), 0, s, H, pl.nb, k, counts, base, stop);
+    hipLaunchKernelGGL(k_big_scan, dim3(1), dim3(1024), 0, s, H, nb, k, counts, base, stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    int nbits = 1;   // bits of the largest label, k - 1
+    while (nbits < 32 && ((uint32_t)(k - 1) >> nbits) != 0u) nbits++;
     if (glob)
-        hipLaunchKernelGGL(k_big_scatter_g, dim3(pl.nb), dim3(256), 0, s, labels, n, k, H, base, perm, stop);
+        hipLaunchKernelGGL(k_big_scatter_g, dim3(nb), dim3(256), 0, s, labels, n, k, nbits, H, base, perm, stop);
     else
-        hipLaunchKernelGGL(k_big_scatter, dim3(pl.nb), dim3(256), (size_t)(k + 256) * 4, s, labels, n, k, H, base,
-                           perm, stop);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_big_scatter, dim3(nb), dim3(256), (size_t)k * 4, s, labels, n, k, nbits, H, base, perm,
+                           stop);
+    return hipGetLastError();
+}
+
+hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
+                               const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
+                               uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
+    if (pl.nb != (int)km_sorted_blocks(n)) return hipErrorInvalidValue;
+    hipError_t e = km_launch_label_sort(labels, n, k, H, counts, base, perm, stop, s);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(C_lite ? k_big_segsum<true> : k_big_segsum<false>, dim3(k), dim3(64 * KB_SEGW),
                        (size_t)KB_SEGW * (d + 1) * 8, s, X, d, best, C_lite, perm, (int64_t)0, counts, base, k, tmp,
                        stop);

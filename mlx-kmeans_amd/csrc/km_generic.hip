@@ -19,7 +19,8 @@
 const char *const km_kernel_names[KK_COUNT] = {
     "km_assign_rows", "km_accum_generic", "km_reduce",     "km_finish",    "km_normalise",
     "km_fused_lowd",  "km_fused_mfma",    "km_big_prep",   "km_big_screen", "km_big_rescore",
-    "km_big_accum",   "km_seed_pp",       "km_relocate"};
+    "km_big_accum",   "km_seed_pp",       "km_relocate",
+    "km_change_sums"};
 
 // Neumaier's compensated add, the reference's KAHAN_ADD (core.py:244-247): t = s + v; the rounding error of
 // that add goes to c; the true running sum is s + c.
@@ -466,8 +467,14 @@ __global__ __launch_bounds__(1024) void k_reduce_finish(const float *__restrict_
 
 __global__ __launch_bounds__(256) void k_finish(const double *__restrict__ tmp, int S, int k, int d,
                                                 double *__restrict__ tot, float *__restrict__ Cnext, int flags,
-                                                const int32_t *__restrict__ stop) {
+                                                const float *__restrict__ Cin, const double *__restrict__ muT,
+                                                const int32_t *__restrict__ dsel, const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
+    __shared__ double red[256];
+    if (dsel && *dsel == 0) {   // the pass chose its change-only sums: one range, added to the previous totals
+        S = 1;
+        flags |= KM_FIN_DELTA | KM_FIN_CENTRED;
+    }
     const int c = blockIdx.x, W = d + 2;
     const int64_t kw = (int64_t)k * W;
     // entry j of this cluster = its S range sums added in ascending order by thread j (and every thread adds the
@@ -480,12 +487,27 @@ __global__ __launch_bounds__(256) void k_finish(const double *__restrict__ tmp, 
     const long long cnt = llrint(cntd);
     const bool update = (flags & KM_FIN_UPDATE) != 0;
     __syncthreads();   // every thread has read the previous count before thread 0 overwrites it
+    const bool centred = (flags & KM_FIN_CENTRED) != 0;
+    double u = 0.0;   // this thread's part of the cluster's centred inertia term
     for (int j = threadIdx.x; j < W; j += 256) {
         double v = 0.0;
         for (int sp = 0; sp < S; sp++) v += src[(int64_t)sp * kw + j];
         if (delta && j != 1) v = tot[(int64_t)c * W + j] + v;   // the previous totals plus their change
         tot[(int64_t)c * W + j] = v;
         if (update && j >= 2 && cnt > 0) Cnext[(int64_t)c * d + (j - 2)] = (float)(v / (double)cnt);
+        if (centred && j >= 2) {   // n |D|^2 - 2 D . (S - n mu), D = c - mu, for this dim
+            const double m = muT[j - 2], D = (double)Cin[(int64_t)c * d + (j - 2)] - m;
+            u += (double)cnt * D * D - 2.0 * D * (v - (double)cnt * m);
+        }
+    }
+    if (centred) {   // the cluster's inertia from the totals (the pass read no row distances): T + sum_c u_c
+        red[threadIdx.x] = u;
+        __syncthreads();
+        for (int h = 128; h > 0; h >>= 1) {
+            if (threadIdx.x < h) red[threadIdx.x] += red[threadIdx.x + h];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) tot[(int64_t)c * W + 1] = red[0] + (c == 0 ? muT[d] : 0.0);
     }
     if (update && (flags & KM_FIN_SPHERICAL) && cnt > 0) {
         __syncthreads();
@@ -514,14 +536,16 @@ hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nr
 }
 
 hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,
-                            int pass, double tol, int flags, const int32_t *stop, hipStream_t s) {
+                            int pass, double tol, int flags, const int32_t *stop, hipStream_t s, const float *Cin,
+                            const double *muT, const int32_t *dsel) {
     const int64_t kw = (int64_t)k * (d + 2);
-    if (kw <= KM_FIN1_MAX && S <= KM_FIN1_SPLITS) {
+    if (((flags & KM_FIN_CENTRED) || dsel) && (!Cin || !muT)) return hipErrorInvalidValue;
+    if (kw <= KM_FIN1_MAX && S <= KM_FIN1_SPLITS && !(flags & KM_FIN_CENTRED) && !dsel) {
         hipLaunchKernelGGL(k_finish1, dim3(1), dim3(1024), (size_t)kw * sizeof(double), s, tmp, S, k, d, tot, Cnext,
                            ctl, pass, tol, flags, stop);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_finish, dim3(k), dim3(256), 0, s, tmp, S, k, d, tot, Cnext, flags, stop);
+    hipLaunchKernelGGL(k_finish, dim3(k), dim3(256), 0, s, tmp, S, k, d, tot, Cnext, flags, Cin, muT, dsel, stop);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !(flags & KM_FIN_UPDATE)) return e;
     hipLaunchKernelGGL(k_stats, dim3(1), dim3(256), 0, s, tot, k, d, Cnext, ctl, pass, tol, stop);

@@ -62,6 +62,7 @@ enum km_kernel_id {
     KK_BIG_ACCUM,
     KK_SEED_PP,
     KK_RELOCATE,
+    KK_CHANGE,   // the wide-row fit loop's change count, gate and change-only sums
     KK_COUNT
 };
 extern const char *const km_kernel_names[KK_COUNT];
@@ -96,8 +97,37 @@ hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb
 #define KM_FIN_SPHERICAL 2
 #define KM_FIN_DELTA 4    // the range sums are the change since the previous pass: added to tot (the inertia
                           // column, column 1, is the pass's own)
+#define KM_FIN_CENTRED 8  // column 1 from the totals: T + sum_c (n_c |c - mu|^2 - 2 (c - mu).(S_c - n_c mu)), with
+                          // the pass's centres Cin and muT = [mu (d), T] (the multi-block finish)
 hipError_t km_launch_finish(const double *tmp, int S, int k, int d, double *tot, float *Cnext, km_control *ctl,
-                            int pass, double tol, int flags, const int32_t *stop, hipStream_t s);
+                            int pass, double tol, int flags, const int32_t *stop, hipStream_t s,
+                            const float *Cin = nullptr, const double *muT = nullptr,
+                            const int32_t *dsel = nullptr);
+// dsel (a gate word of the change-only accumulation): when it reads 0 the finish takes S = 1 change-only range and
+// adds KM_FIN_DELTA | KM_FIN_CENTRED to flags
+// ---- change-only accumulation of the wide-row fit loop (km_wdelta.hip)
+struct km_slice {
+    const float *X;   // the slice's rows
+    int64_t row0;     // its first row in the data set
+};
+int64_t km_wd_blocks(int64_t n);        // count blocks: bcnt takes km_wd_blocks(n) + 1 words
+int64_t km_wd_stat_blocks(int64_t n);   // mean / scatter blocks of one slice
+int km_wd_max_dims();
+// mu (d float64) and T = sum |x - mu|^2 into mu_T[0 .. d]; part: the slices' km_wd_stat_blocks x (d + 1) doubles
+hipError_t km_launch_wd_stats(const km_slice *slices_h, const int64_t *rows, int nslices, int d, double *part,
+                              double *mu_T, hipStream_t s);
+// The changed rows of this pass (lab vs prev over all n rows) and the gate words gate[0] (nonzero: no change-only
+// sums this pass) and gate[1] (nonzero: no full accumulation): change-only when at most `limit` rows changed
+hipError_t km_launch_wd_gate(const uint32_t *lab, const uint32_t *prev, int64_t n, int64_t limit, uint32_t *bcnt,
+                             int32_t *gate, const int32_t *stop, hipStream_t s);
+// The change sums into tmp (k (d + 2), column 1 zero) when gate[0] is 0. elab, erow and perm hold 2 limit words
+// each, H km_sorted_blocks(2 limit) x (k + 1) counters, counts / base k + 1 words, pieces km_wd_piece_doubles;
+// slices_d a device copy of the slice table
+int64_t km_wd_piece_doubles(int64_t limit, int d);
+hipError_t km_launch_wd_accum(const km_slice *slices_d, int nslices, int64_t n, int d, const uint32_t *lab,
+                              const uint32_t *prev, int k, int64_t limit, const uint32_t *bcnt, uint32_t *elab,
+                              uint32_t *erow, uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm,
+                              double *pieces, double *tmp, const int32_t *gate, hipStream_t s);
 hipError_t km_launch_normalise(float *C, int k, int d, hipStream_t s);
 // Streaming read of `bytes` (a multiple of 16) at x by `blocks` blocks of 256 threads; out holds blocks * 256 floats.
 hipError_t km_launch_stream_read(const void *x, int64_t bytes, float *out, int blocks, hipStream_t s);
@@ -212,6 +242,10 @@ hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n,
 // The counting sort by label and per-cluster float64 sums in row order for any rows path (d < 832): rows whose
 // labels and best are known. H holds km_sorted_blocks(n) x k counters; tmp receives the k (d + 2) range sums.
 int64_t km_sorted_blocks(int64_t n);
+// The stable counting sort by label alone: perm lists 0 .. n-1 grouped by label (ascending), ascending within a
+// label; counts / base the k group sizes and starts. H holds km_sorted_blocks(n) x k counters.
+hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32_t *H, uint32_t *counts,
+                                uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32_t *labels, const float *best, int k,
                                   uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *tmp,
                                   const int32_t *stop, hipStream_t s);

@@ -449,7 +449,8 @@ def test_embed_workload_full_size(lib):
 @pytest.mark.parametrize("d,k,parts,path", [(32, 64, 1, "mfma"), (16, 40, 2, "mfma"), (64, 32, 1, "mfma"),
                                             (32, 20, 3, "mfma"), (16, 64, 1, "mfma"), (4, 12, 1, "fused"),
                                             (8, 8, 2, "fused"), (2, 40, 1, "fused"), (3, 30, 3, "fused"),
-                                            (16, 8, 1, "fused"), (1, 200, 1, "fused")])
+                                            (16, 8, 1, "fused"), (1, 200, 1, "fused"), (100, 100, 1, "wide"),
+                                            (128, 300, 2, "wide"), (768, 64, 1, "wide"), (200, 40, 3, "wide")])
 def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts, path):
     """The fit loop accumulates, after its first pass, only the rows whose label changed (into the new cluster, out of
     the old one) and adds that to the previous pass's totals. The same number of Lloyd steps run one at a time with
@@ -457,7 +458,10 @@ def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts, path)
     (within 1e-6), with the same iteration count under a tolerance; reruns of the loop are bit-identical. The data
     keep rows moving between clusters for several passes (overlapping blobs, starting centres drawn from one
     corner). On the fused matrix-core path ("mfma") the loop accumulates only changed rows; on the fused low-d path
-    ("fused", with and without the screen) it accumulates every row each pass, and must agree all the same."""
+    ("fused", with and without the screen) it accumulates every row each pass, and must agree all the same. On the
+    wide-row path ("wide", reported as "mfma") a pass takes the change-only sums when at most n/4 rows changed, and
+    the full accumulation otherwise; its inertia then comes from the totals in centred form. The data make both
+    happen within the passes."""
     rng = np.random.default_rng(900 + d + k + parts)
     n = 90_011
     cen = rng.uniform(-3, 3, size=(k, d)).astype(np.float32)
@@ -473,7 +477,7 @@ def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts, path)
     say(f"[gpu] change accumulation d={d} k={k} parts={parts}")
     C_fit, in_fit, it_fit, _ = ctx.fit(C0, steps, -1.0)
     assert it_fit == steps
-    assert ctx.last_path() == path
+    assert ctx.last_path() == ("mfma" if path == "wide" else path)
     C = C0
     moved = []
     prev_lab = None
@@ -485,6 +489,11 @@ def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts, path)
         C, inertia, _ = ctx.lloyd_step(C)
     say(f"[gpu]   rows changing cluster per pass: {moved}")
     assert sum(moved[:3]) > 0, "the data should move rows between clusters"
+    if path == "wide":
+        limit = n // 4
+        say(f"[gpu]   change-only limit {limit} rows")
+        assert any(0 < m <= limit for m in moved), "some pass should take the change-only sums"
+        assert any(m > limit for m in moved), "some pass should take the full accumulation"
     assert float(np.max(np.abs(C_fit.astype(np.float64) - C.astype(np.float64)))) / scale <= 1e-6
     assert abs(in_fit - inertia) <= 1e-6 * inertia
     C2, in2, _, _ = ctx.fit(C0, steps, -1.0)
