@@ -34,7 +34,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
 static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
-static constexpr int KB_SLICE = 16;       // A-operand K-steps per LDS slice (16 KB)
+static constexpr int KB_SLICE = 25;       // most A-operand K-steps per LDS slice (1 KB each): 768 dims take two
+                                          // slices per chunk, so two block barriers and a prefetch of half a chunk
 static constexpr int KB_WAVES = 4;        // waves per screen block (32 rows each)
 static constexpr int KB_OVER = 0xffff;    // ncand value: scan every centre
 static constexpr double KB_APPROX_LIMIT = 65504.0 / 4;   // the reference's APPROX_FP16_LIMIT (core.py:1035)
@@ -300,7 +301,12 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
         const int s0 = sl * SLK;
         const int ns = (AK - s0) < SLK ? (AK - s0) : SLK;
         for (int j = wave; j < ns; j += KB_WAVES) {
-            const uint16_t *src = Cop + (((int64_t)ch * AK + s0 + j) * 64 + lane) * 8;
+            // the K-step's base is wave-uniform: kept in scalar registers (the saddr form of the load), so the
+            // ring costs one lane-offset VGPR instead of a 64-bit address per slice
+            const uint64_t bse = (uint64_t)(uintptr_t)(Cop + ((int64_t)ch * AK + s0 + j) * 64 * 8);
+            const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)bse);
+            const uint32_t bhi = __builtin_amdgcn_readfirstlane((uint32_t)(bse >> 32));
+            const uint16_t *src = (const uint16_t *)(uintptr_t)(((uint64_t)bhi << 32) | blo) + lane * 8;
             __builtin_amdgcn_global_load_lds((gbl_vptr)src, (lds_vptr)(buf + j * 1024), 16, 0, 0);
         }
     };
@@ -314,14 +320,28 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (g + 1 < G) issue(g + 1);
+            // A fragments three K-steps ahead of their MFMA (four registers sets in rotation), the reads and MFMAs
+            // interleaved one for one: the LDS latency is covered by three MFMAs instead of two
+            bf16x8 Ab[4];
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+                if (sl * SLK + j < AK && j < SLK) Ab[j] = *reinterpret_cast<const bf16x8 *>(cur + j * 1024 + lane * 16);
 #pragma unroll
             for (int j = 0; j < SLK; j++) {
                 const int s = sl * SLK + j;   // compile-time after unrolling
-                if (s < AK) {
-                    const bf16x8 A = *reinterpret_cast<const bf16x8 *>(cur + j * 1024 + lane * 16);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, s < DS ? B[s < DS ? s : 0] : Bone, acc, 0, 0, 0);
-                }
+                if (j + 3 < SLK && s + 3 < AK)
+                    Ab[(j + 3) & 3] = *reinterpret_cast<const bf16x8 *>(cur + (j + 3) * 1024 + lane * 16);
+                if (s < AK)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Ab[j & 3], s < DS ? B[s < DS ? s : 0] : Bone, acc, 0,
+                                                                   0, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);   // three LDS reads,
+#pragma unroll
+            for (int j = 0; j < SLK - 3; j++) {                    // then MFMA, LDS read, ...,
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // and the last three MFMAs
         }
     };
 
@@ -1076,7 +1096,12 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
     // exact=False approximates from 64 dims, and only under the half-precision guard (checked in the kernel);
     // below 64 dims the reference's dispatch runs its exact kernels (core.py:2036-2042)
     const int approx = (mode == KM_APPROX && d >= KM_APPROX_MIN_DIMS) ? 1 : 0;
-    const size_t lds = 2 * KB_SLICE * 1024 + KB_WAVES * KB_HALF * 64 * (pack ? 4 : 6);
+    const int ak = pl.DS + 1, spc = (ak + KB_SLICE - 1) / KB_SLICE, slk = (ak + spc - 1) / spc;
+    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * KB_HALF * 64 * (pack ? 4 : 6);
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), lds, s, X16T,
                        xsq, n, d, Cop, maxes, k, pl.nchunks, pl.ib, rho, approx, xmax, ncand, cand, over, multi, ctl,
                        stop);
