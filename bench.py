@@ -254,7 +254,8 @@ def main():
                            "max": round(float(pass_ms.max()), 5), "first": round(float(pass_ms[0]), 5),
                            "passes": int(len(pass_ms)),
                            "note": "HIP events at every pass boundary of a second timed loop; the first pass of "
-                                   "a fit accumulates every row, later passes only the rows whose label changed"},
+                                   "a fit accumulates every row, later passes only the rows whose label changed "
+                                   "(on the wide-row path, when at most a quarter of the rows changed)"},
         "stream_read_gbs": round(stream_gbs, 1),
         "final_inertia": inertia,
         "roofline": roof,
