@@ -78,6 +78,7 @@ struct km_ctx {
     DBuf<uint16_t> ncand;
     DBuf<uint16_t> cand;
     DBuf<uint32_t> hist, counts, base, perm, over, multi;
+    DBuf<uint64_t> okeys;   // wide-row path: the overflow rows' (best, label) keys of the split full scan
     DBuf<uint32_t> xmax;    // wide-row path: the largest |x|^2 over every slice (float bits)
     DBuf<uint8_t> lstate;   // the fit loop's label of every row (one byte; each slice at lstate_off[i])
     std::vector<int64_t> lstate_off;
@@ -250,6 +251,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->perm.release();
     c->over.release();
     c->multi.release();
+    c->okeys.release();
     c->xmax.release();
     c->lstate.release();
     c->red.release();
@@ -479,6 +481,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, c->perm.ensure((size_t)max_rows));
     HIPCHK(c, c->over.ensure((size_t)max_rows));
     HIPCHK(c, c->multi.ensure((size_t)max_rows));
+    HIPCHK(c, c->okeys.ensure((size_t)max_rows));
     HIPCHK(c, c->labels.ensure((size_t)c->n));
     HIPCHK(c, c->best.ensure((size_t)c->n));
     HIPCHK(c, c->tot.ensure((size_t)kw));
@@ -510,7 +513,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
         }));
         HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {
             return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->multi.p,
-                                         c->ctl, lab_all + row0, best_all + row0, lite, stop, c->stream);
+                                         c->ctl, lab_all + row0, best_all + row0, lite, c->okeys.p, stop, c->stream);
         }));
         row0 += p.rows;
     }

@@ -658,10 +658,6 @@ __global__ __launch_bounds__(256) void k_big_label1(const uint16_t *__restrict__
     if (code != KB_OVER && (code & 255) + (code >> 8) == 1) labels[r] = cand[r * KB_CAP + ((code & 255) ? 0 : KB_HALF)];
 }
 
-// Block per listed row: the rows loop over every centre. The row sits in LDS; 256 centres at a time are staged
-// 32 dims per chunk (coalesced), thread t carrying the direct-form sum of centre c0 + t; each thread keeps its
-// smallest value over its centres (ascending, strict '<'), then the block keeps the smallest value, lowest index
-// among equal values - the rows loop's label and best.
 // Rows the screen could not narrow (more than KB_HALF window centres in a half-row, or non-finite data) take the
 // rows loop over every centre. Blocks of 256 threads take 64 listed rows at a time against chunks of 64 centres:
 // 32 dims of the rows and of the centres staged in LDS per step, each thread carrying 4 rows x 4 centres of
@@ -669,12 +665,20 @@ __global__ __launch_bounds__(256) void k_big_label1(const uint16_t *__restrict__
 // the smallest distance with a strict '<' over its centres in ascending order. The 16 threads that share a row
 // then reduce (value, index) with the lowest index on ties: the rows loop's label and best, label 0 and best +inf
 // included when no distance compares below +inf.
-static constexpr int KB_FR = 64;      // rows per full-scan tile
-static constexpr int KB_FC = 64;      // centres per full-scan chunk
+// Above KB_FSPLIT centres the centres are split into ranges of KB_FSPLIT, one block per (tile, range), so that a
+// handful of listed rows still spreads over the chip. Each range's result (value, index) goes into the row's 64-bit
+// key by an atomic minimum of (value bits << 32 | index): distances are non-negative or NaN, NaN is never taken
+// (strict '<'), so the key order is the value order and then the index order - the smallest distance, the lowest
+// index among equal ones, whatever order the ranges finish in. The key starts at (+inf, 0).
+static constexpr int KB_FR = 64;        // rows per full-scan tile
+static constexpr int KB_FC = 64;        // centres per full-scan chunk
+static constexpr int KB_FSPLIT = 256;   // centres per range of the split full scan
+static constexpr uint64_t KB_FKEY0 = (uint64_t)0x7f800000u << 32;   // (+inf, label 0)
 __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ X, int d, const float *__restrict__ C,
                                                       int k, const uint32_t *__restrict__ over,
                                                       km_control *__restrict__ ctl, uint32_t *__restrict__ labels,
-                                                      float *__restrict__ best, const int32_t *__restrict__ stop) {
+                                                      float *__restrict__ best, uint64_t *__restrict__ keys,
+                                                      const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
     __shared__ float xs[KB_RCH][KB_FR + 1];   // [dim][row]
     __shared__ float cs[KB_RCH][KB_FC + 1];   // [dim][centre]
@@ -683,7 +687,14 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
     const int tr = tid >> 4, tc = tid & 15;   // rows 4 tr .. 4 tr + 3, centres 4 tc .. 4 tc + 3 of a chunk
     const uint32_t total = ctl->n_over;
     if (blockIdx.x == 0 && tid == 0) atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)total);
-    for (uint32_t t0 = blockIdx.x * KB_FR; t0 < total; t0 += gridDim.x * KB_FR) {
+    // work items: (tile, range) pairs, ranges of KB_FSPLIT centres when keys are given, else one range of all
+    const int nsplit = keys ? (k + KB_FSPLIT - 1) / KB_FSPLIT : 1;
+    const int csplit = keys ? KB_FSPLIT : k;
+    const uint64_t items = (uint64_t)((total + KB_FR - 1) / KB_FR) * (uint64_t)nsplit;
+    for (uint64_t p = blockIdx.x; p < items; p += gridDim.x) {
+        const uint32_t t0 = (uint32_t)(p / (uint64_t)nsplit) * KB_FR;
+        const int cbeg = (int)(p % (uint64_t)nsplit) * csplit;
+        const int cend = (cbeg + csplit < k) ? cbeg + csplit : k;
         const int nr = (int)((total - t0) < (uint32_t)KB_FR ? (total - t0) : (uint32_t)KB_FR);
         __syncthreads();   // the previous tile's rows are no longer read
         if (tid < KB_FR) rows[tid] = tid < nr ? (int64_t)over[t0 + tid] : (int64_t)over[t0];
@@ -695,7 +706,7 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
             bst[a] = INFINITY;
             bl[a] = 0u;
         }
-        for (int c0 = 0; c0 < k; c0 += KB_FC) {
+        for (int c0 = cbeg; c0 < cend; c0 += KB_FC) {
             float sacc[4][4];
 #pragma unroll
             for (int a = 0; a < 4; a++)
@@ -710,7 +721,7 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
                 }
                 for (int e = tid; e < KB_FC * KB_RCH; e += 256) {
                     const int c = e / KB_RCH, jj = e - (e / KB_RCH) * KB_RCH;
-                    cs[jj][c] = (jj < w && c0 + c < k) ? C[(int64_t)(c0 + c) * d + j0 + jj] : 0.0f;
+                    cs[jj][c] = (jj < w && c0 + c < cend) ? C[(int64_t)(c0 + c) * d + j0 + jj] : 0.0f;
                 }
                 __syncthreads();
                 for (int jj = 0; jj < w; jj++) {
@@ -731,7 +742,7 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const int c = c0 + 4 * tc + b;
-                if (c < k) {
+                if (c < cend) {
 #pragma unroll
                     for (int a = 0; a < 4; a++)
                         if (sacc[a][b] < bst[a]) {
@@ -756,10 +767,37 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
             }
             const int r = 4 * tr + a;
             if (tc == 0 && r < nr) {
-                labels[rows[r]] = ix;
-                best[rows[r]] = v;
+                if (keys) {
+                    if (v < INFINITY)
+                        atomicMin((unsigned long long *)&keys[t0 + r],
+                                  (unsigned long long)(((uint64_t)__float_as_uint(v) << 32) | ix));
+                } else {
+                    labels[rows[r]] = ix;
+                    best[rows[r]] = v;
+                }
             }
         }
+    }
+}
+
+// The split full scan's keys: (+inf, 0) for every listed row before, its label and best after.
+__global__ __launch_bounds__(256) void k_big_fkeys_init(uint64_t *__restrict__ keys, const km_control *__restrict__ ctl,
+                                                        const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const uint32_t total = ctl->n_over;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) keys[i] = KB_FKEY0;
+}
+
+__global__ __launch_bounds__(256) void k_big_fkeys_fin(const uint64_t *__restrict__ keys,
+                                                       const uint32_t *__restrict__ over,
+                                                       const km_control *__restrict__ ctl, uint32_t *__restrict__ labels,
+                                                       float *__restrict__ best, const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    const uint32_t total = ctl->n_over;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+        const uint64_t key = keys[i];
+        labels[over[i]] = (uint32_t)key;
+        best[over[i]] = __uint_as_float((uint32_t)(key >> 32));
     }
 }
 
@@ -1110,7 +1148,8 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
 
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
-                                 uint32_t *labels, float *best, int lite, const int32_t *stop, hipStream_t s) {
+                                 uint32_t *labels, float *best, int lite, uint64_t *okeys, const int32_t *stop,
+                                 hipStream_t s) {
     const bool v4 = (d % 4 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)C % 16 == 0);
     const unsigned chunks = (unsigned)((n + KB_RR - 1) / KB_RR);
     hipError_t e;
@@ -1129,8 +1168,16 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
                            ctl, labels, best, stop);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, ctl, labels, best,
-                       stop);
+    if (k <= KB_FSPLIT || !okeys) {
+        hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, ctl, labels, best,
+                           (uint64_t *)nullptr, stop);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_big_fkeys_init, dim3(256), dim3(256), 0, s, okeys, ctl, stop);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, ctl, labels, best, okeys, stop);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_big_fkeys_fin, dim3(256), dim3(256), 0, s, okeys, over, ctl, labels, best, stop);
     return hipGetLastError();
 }
 

@@ -231,10 +231,12 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
                                 const uint32_t *xmax, int64_t n, int d, const uint16_t *Cop, const float *maxes, int k,
                                 uint16_t *ncand, uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
                                 const int32_t *stop, hipStream_t s);
-// lite: the pass returns no per-row distances; single-candidate rows take their label without one
+// lite: the pass returns no per-row distances; single-candidate rows take their label without one. okeys: n words
+// for the full scan of the overflow rows split over centre ranges (above 256 centres; null: one range)
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
-                                 uint32_t *labels, float *best, int lite, const int32_t *stop, hipStream_t s);
+                                 uint32_t *labels, float *best, int lite, uint64_t *okeys, const int32_t *stop,
+                                 hipStream_t s);
 // C_lite non-null: the best column is the rows' FMA-form distances to C, not best[] (pair with a lite rescore)
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,

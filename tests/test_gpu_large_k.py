@@ -107,3 +107,33 @@ def test_large_k_at_the_references_size(lib):
     say(f"[gpu]   fit passes (ms): {' '.join(f'{v:.1f}' for v in t)}")
     assert n_iter == 3
     ctx.close()
+
+
+@pytest.mark.parametrize("k,d", [(1000, 64), (5000, 40)])
+def test_overflow_rows_scan_every_centre_range(lib, k, d):
+    """Rows whose window holds more than 16 centres of a half-row take the full scan, which above 256 centres splits
+    the centres into ranges over many blocks and keeps, per row, the smallest distance and the lowest index among
+    equal ones. Here 40 identical centres sit on one blob's mean (indices 300-339), so every row of that blob
+    overflows and must take label 300; two rows are NaN (the rows loop gives them label 0 and best +inf)."""
+    import oracle
+    rng = np.random.default_rng(k + d)
+    n = 20_000
+    blobs = rng.uniform(-20, 20, (5, d)).astype(np.float32)
+    X = (blobs[rng.integers(0, 5, n)] + 0.3 * rng.standard_normal((n, d))).astype(np.float32)
+    X[[7, 12_345]] = np.nan
+    C = rng.uniform(60, 90, (k, d)).astype(np.float32)
+    C[300:340] = blobs[0]
+    C[10:14] = blobs[1:5]
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] overflow rows: n={n} d={d} k={k}")
+    tot, labels, best = ctx.run_pass(C, labels=True, best=True)
+    over = ctx.fallback_rows()
+    say(f"[gpu]   rows scored against every centre: {over}")
+    assert over >= 3000                  # the blob on the 40 copies: about a fifth of the rows
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(labels, ol), np.flatnonzero(labels != ol)[:10]
+    assert np.array_equal(best.view(np.uint32), ob.view(np.uint32))
+    assert labels[7] == 0 and best[7] == np.inf
+    assert (labels == 300).sum() > 3000
+    ctx.close()
