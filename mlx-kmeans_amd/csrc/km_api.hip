@@ -104,7 +104,7 @@ struct km_ctx {
     DBuf<uint32_t> wd_H, wd_cnt, wd_base, wd_perm;   // the entries' counting sort by label (k + 1 labels)
     DBuf<int32_t> wd_gate;          // [0] nonzero: no change-only sums this pass; [1] nonzero: no full accumulation
     DBuf<double> wd_part, wd_mu;    // mean / scatter partials; [mu (d), T] of the data set
-    DBuf<double> wd_pieces;         // the change sums of clusters that span several chunks, per chunk
+    DBuf<double> pieces;            // the sums of clusters whose sorted rows span several chunks, per chunk
     DBuf<km_slice> wd_slices;       // the slice table on the device
     std::vector<km_slice> wd_slices_h;
     bool wd_ready = false;          // wd_mu and wd_slices describe the current data
@@ -268,7 +268,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->wd_cnt.release();
     c->wd_base.release();
     c->wd_perm.release();
-    c->wd_pieces.release();
+    c->pieces.release();
     c->wd_gate.release();
     c->wd_part.release();
     c->wd_mu.release();
@@ -481,6 +481,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, c->perm.ensure((size_t)max_rows));
     HIPCHK(c, c->over.ensure((size_t)max_rows));
     HIPCHK(c, c->multi.ensure((size_t)max_rows));
+    HIPCHK(c, c->pieces.ensure((size_t)km_chunk_piece_doubles(max_rows, d, 0)));
     HIPCHK(c, c->okeys.ensure((size_t)max_rows));
     HIPCHK(c, c->labels.ensure((size_t)c->n));
     HIPCHK(c, c->best.ensure((size_t)c->n));
@@ -530,8 +531,8 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
         const km_big_plan bp = km_plan_big(p.rows, d, k);
         HIPCHK(c, launch(c, KK_BIG_ACCUM, [&] {
             return km_launch_big_accum(bp, p.X, p.rows, d, lab_all + row0, best_all + row0, lite ? Cin : nullptr, k,
-                                       c->hist.p, c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw,
-                                       full_gate, c->stream);
+                                       c->hist.p, c->counts.p, c->base.p, c->perm.p, c->pieces.p,
+                                       c->red.p + (int64_t)i * kw, full_gate, c->stream);
         }));
         row0 += p.rows;
     }
@@ -539,7 +540,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, launch(c, KK_CHANGE, [&] {
         return km_launch_wd_accum(c->wd_slices.p, (int)c->parts.size(), c->n, d, lab_all, lab_prev, k, c->wd_limit,
                                   c->wd_bcnt.p, c->wd_e.p, c->wd_e.p + 2 * c->wd_limit, c->wd_H.p, c->wd_cnt.p,
-                                  c->wd_base.p, c->wd_perm.p, c->wd_pieces.p, c->red.p, c->wd_gate.p, c->stream);
+                                  c->wd_base.p, c->wd_perm.p, c->pieces.p, c->red.p, c->wd_gate.p, c->stream);
     }));
     return finish_pass(c, k, 0, pass, tol, flags, stop, S, c->wd_gate.p);
 }
@@ -628,6 +629,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         HIPCHK(c, c->counts.ensure((size_t)k));
         HIPCHK(c, c->base.ensure((size_t)k));
         HIPCHK(c, c->perm.ensure((size_t)max_rows));
+        HIPCHK(c, c->pieces.ensure((size_t)km_chunk_piece_doubles(max_rows, d, 0)));
         HIPCHK(c, c->tot.ensure((size_t)kw));
         const int S = (int)c->parts.size();
         HIPCHK(c, c->red.ensure((size_t)S * kw));
@@ -641,8 +643,8 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             }));
             HIPCHK(c, launch(c, KK_ACCUM_GENERIC, [&] {
                 return km_launch_sorted_accum(p.X, p.rows, d, lab_all + row0, best_all + row0, k, c->hist.p,
-                                              c->counts.p, c->base.p, c->perm.p, c->red.p + (int64_t)i * kw, stop,
-                                              c->stream);
+                                              c->counts.p, c->base.p, c->perm.p, c->pieces.p,
+                                              c->red.p + (int64_t)i * kw, stop, c->stream);
             }));
             row0 += p.rows;
         }
@@ -838,7 +840,10 @@ static int prepare_wide_delta(km_ctx *c, int k, bool *use) {
     HIPCHK(c, c->wd_cnt.ensure((size_t)k + 1));
     HIPCHK(c, c->wd_base.ensure((size_t)k + 1));
     HIPCHK(c, c->wd_perm.ensure((size_t)limit * 2));
-    HIPCHK(c, c->wd_pieces.ensure((size_t)km_wd_piece_doubles(limit, d)));
+    int64_t max_rows = 0;
+    for (auto &p : c->parts) max_rows = std::max(max_rows, p.rows);
+    HIPCHK(c, c->pieces.ensure((size_t)std::max(km_chunk_piece_doubles(2 * limit, d, 2),
+                                                 km_chunk_piece_doubles(max_rows, d, 0))));
     HIPCHK(c, c->wd_gate.ensure(2));
     if (!c->wd_ready) {
         std::vector<int64_t> rows;

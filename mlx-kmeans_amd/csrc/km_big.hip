@@ -12,8 +12,8 @@
 //   k_big_rescore   the rows loop (core.py:263-274) on those candidates only, ascending index, strict '<'
 //   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every
 //                   centre, 64 rows x 64 centres per block step
-//   k_big_hist/scan/scatter/segsum   a stable counting sort of the rows by label and per-cluster sums in row
-//                   order (float64), the totals of the pass
+//   k_big_hist/scan/scatter   a stable counting sort of the rows by label; then the per-cluster float64 sums in
+//                   row order, in fixed chunks of sorted rows (km_chunks.hip): the totals of the pass
 //
 // Labels and best are the rows loop's bit for bit (see the window below). With mode KM_APPROX the screen's
 // minimiser is taken on trust, as the reference's exact=False path does (core.py:878-890, 1061-1088), only its
@@ -805,10 +805,10 @@ __global__ __launch_bounds__(256) void k_big_fkeys_fin(const uint64_t *__restric
 //
 // A stable counting sort of the rows by label: per 4096-row block a histogram (LDS integer adds, exact), per
 // label an exclusive prefix over blocks on top of the labels before it, then each block places its rows in
-// ascending row order (rank among earlier rows of the same label in the block). Each cluster then sums its
-// rows in that order - ascending row index - in float64: 16 waves take 16 fixed consecutive ranges of the
-// cluster's rows, lanes take dims, and the wave sums are added in wave order. Count, best sum and coordinate
-// sums land as one range sum per entry (tmp, S = 1 per slice), the format the finish reads.
+// ascending row order (rank among earlier rows of the same label in the block). The clusters' float64 sums over
+// their rows in that order come from km_chunks.hip (fixed chunks of sorted rows per wave, so an uneven split of
+// the rows among the clusters costs nothing). Count, best sum and coordinate sums land as one range sum per entry
+// (tmp, S = 1 per slice), the format the finish reads.
 
 static constexpr int KB_RB = 4096;   // rows per histogram / scatter block
 
@@ -945,105 +945,6 @@ __global__ __launch_bounds__(256) void k_big_scatter_g(const uint32_t *__restric
                                                        const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
     kb_scatter_body<true>(labels, n, nbits, O + (int64_t)blockIdx.x * k, base, perm);
-}
-
-// Block per cluster (KB_SEGW waves, each a fixed consecutive range of the cluster's rows): entries [count, best,
-// x_0 .. x_{d-1}] as float64 sums over the cluster's rows in ascending row order, written to tmp[c * (d + 2) + e].
-// With LITE the best column is not read from best[]: each lane adds (x_j - c_j)^2 over its dims for every row (FMA
-// form, float32 per row, float64 across rows) and the wave adds its lanes in a fixed butterfly - the cluster's
-// inertia, equal to the sum of the rows' direct-form distances to float32 rounding.
-static constexpr int KB_SEGW = 8;
-template <bool LITE>
-__global__ __launch_bounds__(64 * KB_SEGW) void k_big_segsum(const float *__restrict__ X, int d, const float *__restrict__ best,
-                                                     const float *__restrict__ C,
-                                                     const uint32_t *__restrict__ perm, int64_t r0,
-                                                     const uint32_t *__restrict__ counts,
-                                                     const uint32_t *__restrict__ base, int k,
-                                                     double *__restrict__ tmp, const int32_t *__restrict__ stop) {
-    if (stop && *stop) return;
-    extern __shared__ double part[];   // KB_SEGW waves x (d + 1)
-    const int c = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t cnt = counts[c], b0 = base[c];
-    const uint32_t q0 = b0 + (uint32_t)((uint64_t)cnt * wave / KB_SEGW);
-    const uint32_t q1 = b0 + (uint32_t)((uint64_t)cnt * (wave + 1) / KB_SEGW);
-    const int W = d + 2;
-    double *mine = part + (size_t)wave * (d + 1);
-    // lane owns dims lane, lane + 64, ...; dim d (the best column) is kept by lane d % 64 as the extra slot
-    constexpr int MAXJ = 13;   // dims per lane: ceil(769 / 64)
-    double acc[MAXJ];
-#pragma unroll
-    for (int i = 0; i < MAXJ; i++) acc[i] = 0.0;
-    float cv[LITE ? MAXJ : 1];
-    double accb = 0.0;
-    if constexpr (LITE) {
-#pragma unroll
-        for (int i = 0; i < MAXJ; i++) {
-            const int j = lane + 64 * i;
-            cv[i] = j < d ? C[(int64_t)c * d + j] : 0.0f;
-        }
-    }
-    // rows in order; the row indices of the next 8 are loaded ahead, and each row's values are loaded before
-    // they are added
-    uint32_t pf[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) pf[u] = q0 + u < q1 ? perm[q0 + u] : 0u;
-    for (uint32_t q = q0; q < q1; q += 8) {
-        uint32_t cur[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) cur[u] = pf[u];
-#pragma unroll
-        for (int u = 0; u < 8; u++) pf[u] = q + 8 + u < q1 ? perm[q + 8 + u] : 0u;
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            if (q + u < q1) {
-                const int64_t r = r0 + cur[u];
-                const float *x = X + r * d;
-                // unconditional loads (a lane past the last dim reads dim d - 1), masked afterwards: a guarded load
-                // becomes a branch of its own
-                float v[MAXJ];
-#pragma unroll
-                for (int i = 0; i < MAXJ; i++) v[i] = x[min(lane + 64 * i, d - 1)];
-                const float bv = LITE ? 0.0f : best[r];
-#pragma unroll
-                for (int i = 0; i < MAXJ; i++) {
-                    const int j = lane + 64 * i;
-                    if (j >= d) v[i] = (!LITE && j == d) ? bv : 0.0f;
-                }
-#pragma unroll
-                for (int i = 0; i < MAXJ; i++) acc[i] += (double)v[i];
-                if constexpr (LITE) {
-                    float ds = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < MAXJ; i++) {
-                        const float t = v[i] - cv[i];   // 0 - 0 past the last dim
-                        ds = __builtin_fmaf(t, t, ds);
-                    }
-                    accb += (double)ds;
-                }
-            }
-        }
-    }
-    if constexpr (LITE) {
-        for (int off = 32; off > 0; off >>= 1) accb += __shfl_xor(accb, off);
-#pragma unroll
-        for (int i = 0; i < MAXJ; i++)
-            if (lane + 64 * i == d) acc[i] = accb;
-    }
-#pragma unroll
-    for (int i = 0; i < MAXJ; i++) {
-        const int j = lane + 64 * i;
-        if (j <= d) mine[j] = acc[i];
-    }
-    __syncthreads();
-    for (int j = threadIdx.x; j <= d; j += 64 * KB_SEGW) {
-        double t = 0.0;
-        for (int w = 0; w < KB_SEGW; w++) t += part[(size_t)w * (d + 1) + j];
-        // column order [count, best, x...]
-        if (j < d) tmp[(int64_t)c * W + 2 + j] = t;
-        else tmp[(int64_t)c * W + 1] = t;
-    }
-    if (threadIdx.x == 0) tmp[(int64_t)c * W] = (double)cnt;
 }
 
 // ------------------------------------------------------------------ planning and launch
@@ -1184,12 +1085,12 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
 int64_t km_sorted_blocks(int64_t n) { return (n + KB_RB - 1) / KB_RB; }
 
 hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32_t *labels, const float *best, int k,
-                                  uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *tmp,
-                                  const int32_t *stop, hipStream_t s) {
-    if (d < 1 || d > 64 * 13 - 1) return hipErrorInvalidValue;
+                                  uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *pieces,
+                                  double *tmp, const int32_t *stop, hipStream_t s) {
+    if (d < 1 || d > KM_CHUNK_MAX_DIMS) return hipErrorInvalidValue;
     km_big_plan pl{};
     pl.nb = (int)km_sorted_blocks(n);
-    return km_launch_big_accum(pl, X, n, d, labels, best, nullptr, k, H, counts, base, perm, tmp, stop, s);
+    return km_launch_big_accum(pl, X, n, d, labels, best, nullptr, k, H, counts, base, perm, pieces, tmp, stop, s);
 }
 
 hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32_t *H, uint32_t *counts,
@@ -1222,12 +1123,11 @@ hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32
 
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
-                               uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s) {
+                               uint32_t *base, uint32_t *perm, double *pieces, double *tmp, const int32_t *stop,
+                               hipStream_t s) {
     if (pl.nb != (int)km_sorted_blocks(n)) return hipErrorInvalidValue;
     hipError_t e = km_launch_label_sort(labels, n, k, H, counts, base, perm, stop, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(C_lite ? k_big_segsum<true> : k_big_segsum<false>, dim3(k), dim3(64 * KB_SEGW),
-                       (size_t)KB_SEGW * (d + 1) * 8, s, X, d, best, C_lite, perm, (int64_t)0, counts, base, k, tmp,
-                       stop);
-    return hipGetLastError();
+    return km_launch_chunk_sums(C_lite ? 1 : 0, X, nullptr, 0, d, labels, nullptr, best, C_lite, perm, counts, base, k,
+                                nullptr, n, pieces, tmp, stop, s);
 }

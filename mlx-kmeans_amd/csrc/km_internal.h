@@ -121,9 +121,8 @@ hipError_t km_launch_wd_stats(const km_slice *slices_h, const int64_t *rows, int
 hipError_t km_launch_wd_gate(const uint32_t *lab, const uint32_t *prev, int64_t n, int64_t limit, uint32_t *bcnt,
                              int32_t *gate, const int32_t *stop, hipStream_t s);
 // The change sums into tmp (k (d + 2), column 1 zero) when gate[0] is 0. elab, erow and perm hold 2 limit words
-// each, H km_sorted_blocks(2 limit) x (k + 1) counters, counts / base k + 1 words, pieces km_wd_piece_doubles;
-// slices_d a device copy of the slice table
-int64_t km_wd_piece_doubles(int64_t limit, int d);
+// each, H km_sorted_blocks(2 limit) x (k + 1) counters, counts / base k + 1 words, pieces
+// km_chunk_piece_doubles(2 limit, d, 2); slices_d a device copy of the slice table
 hipError_t km_launch_wd_accum(const km_slice *slices_d, int nslices, int64_t n, int d, const uint32_t *lab,
                               const uint32_t *prev, int k, int64_t limit, const uint32_t *bcnt, uint32_t *elab,
                               uint32_t *erow, uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm,
@@ -240,7 +239,22 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
 // C_lite non-null: the best column is the rows' FMA-form distances to C, not best[] (pair with a lite rescore)
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
-                               uint32_t *base, uint32_t *perm, double *tmp, const int32_t *stop, hipStream_t s);
+                               uint32_t *base, uint32_t *perm, double *pieces, double *tmp, const int32_t *stop,
+                               hipStream_t s);
+// ---- per-cluster sums over rows listed in cluster order, in fixed chunks (km_chunks.hip)
+#define KM_CHUNK_MAX_DIMS 832
+// pieces for npos listed positions: mode 0 (rows, best[] column) and 1 (rows, distances to C), mode 2 (change
+// entries)
+int64_t km_chunk_piece_doubles(int64_t npos, int d, int mode);
+// The k (d + 2) sums into tmp: [count, best column, x] per cluster, from the positions perm lists in label order
+// (counts / base per label). Modes 0 / 1: rows of X (perm holds row indices; lab, best per row; npos rows).
+// Mode 2: change entries (perm holds entry indices; lab, erow per entry, rows found in the device slice table;
+// 2 *npos_dev positions). gate (may be null): nonzero skips the work.
+hipError_t km_launch_chunk_sums(int mode, const float *X, const km_slice *slices, int nslices, int d,
+                                const uint32_t *lab, const uint32_t *erow, const float *best, const float *C,
+                                const uint32_t *perm, const uint32_t *counts, const uint32_t *base, int k,
+                                const uint32_t *npos_dev, int64_t npos, double *pieces, double *tmp,
+                                const int32_t *gate, hipStream_t s);
 // The counting sort by label and per-cluster float64 sums in row order for any rows path (d < 832): rows whose
 // labels and best are known. H holds km_sorted_blocks(n) x k counters; tmp receives the k (d + 2) range sums.
 int64_t km_sorted_blocks(int64_t n);
@@ -249,8 +263,8 @@ int64_t km_sorted_blocks(int64_t n);
 hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32_t *H, uint32_t *counts,
                                 uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32_t *labels, const float *best, int k,
-                                  uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *tmp,
-                                  const int32_t *stop, hipStream_t s);
+                                  uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *pieces,
+                                  double *tmp, const int32_t *stop, hipStream_t s);
 // Centres above which the rows path accumulates through the counting sort (the generic accumulation re-reads the
 // rows once per block of clusters)
 #define KM_SORTED_MIN_K 4096

@@ -5,9 +5,8 @@
 // that changed are listed in row order over all slices (per-block counts, an exclusive scan over the blocks,
 // in-block ranks), each giving two entries (its new label with +row, its old label with -row); the entries are
 // sorted by label with the counting sort of the full accumulation (stable: entry order within a label), and the
-// sorted entries are added in fixed chunks of 64, one wave each, lanes owning dims, in float64, the clusters that
-// span chunks combined from per-chunk pieces in chunk order. A pass then reads only the changed rows instead of
-// every row.
+// sorted entries are added in fixed chunks of 64, one wave each, in float64 (km_chunks.hip). A pass then reads
+// only the changed rows instead of every row.
 //
 // Each pass chooses on the device: the scan of the counts compares the number of changed rows m with a limit set
 // by the host (up to which sorting 2 limit entries and reading 2m rows costs less than the full accumulation) and
@@ -25,8 +24,6 @@ namespace {
 
 constexpr int WD_RB = 4096;   // rows per block of the change count and the entry list
 constexpr int WD_SB = 512;    // rows per block of the mean and scatter
-constexpr int WD_Q = 64;      // sorted entries per wave of the change sums
-constexpr int WD_MAXJ = 13;   // dims per lane in the change sums: d <= 832
 
 // Block b of rows [b WD_SB, ...) of one slice: mode 0 the float64 column sums into part[b][0 .. d); mode 1 the
 // block's sum of (x - mu)^2 into part[b][d]. With d <= 256 the block's threads form G = 256 / d row groups of d
@@ -205,150 +202,11 @@ __global__ __launch_bounds__(256) void k_wd_pad(uint32_t *__restrict__ elab, int
     for (int64_t e = e0 + (int64_t)blockIdx.x * 256 + threadIdx.x; e < len; e += (int64_t)gridDim.x * 256) elab[e] = k;
 }
 
-typedef __attribute__((address_space(1))) float gfloat;
-
-// A row's address from its entry (the slice table lists ascending first rows).
-__device__ __forceinline__ const float *wd_row(const km_slice *__restrict__ slices, int nslices, int d, uint32_t er) {
-    const int64_t r = (int64_t)(er & 0x7fffffffu);
-    int s = 0;
-    while (s + 1 < nslices && slices[s + 1].row0 <= r) s++;
-    return slices[s].X + (r - slices[s].row0) * d;
-}
-
-// The change sums over the sorted entries in chunks of WD_Q: wave q takes sorted positions [q WD_Q, (q + 1) WD_Q) of
-// the 2m valid ones (each cluster's run is contiguous, in entry order), loads their row addresses lane-parallel,
-// then adds the rows in position order, four in flight, into float64 sums (lane owns dims lane, lane + 64, ...),
-// closing a piece at every change of cluster. A cluster whose run lies inside the chunk is complete: written to tmp
-// as [count, 0, x]. A cluster that runs past the chunk's edge leaves a piece: the head slot of the chunk for the
-// cluster holding its first position, the tail slot for the one holding its last. Every wave does the same amount
-// of work, however unevenly the changed rows fall among the clusters.
-__global__ __launch_bounds__(256) void k_wd_chunks(const km_slice *__restrict__ slices, int nslices, int d,
-                                                   const uint32_t *__restrict__ elab, const uint32_t *__restrict__ erow,
-                                                   const uint32_t *__restrict__ perm,
-                                                   const uint32_t *__restrict__ counts,
-                                                   const uint32_t *__restrict__ base,
-                                                   const uint32_t *__restrict__ mcount, double *__restrict__ pieces,
-                                                   double *__restrict__ tmp, const int32_t *__restrict__ gate) {
-    if (*gate) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t q = (int64_t)blockIdx.x * 4 + wave;
-    const int64_t E = 2 * (int64_t)*mcount;
-    const int64_t e0 = q * WD_Q;
-    if (e0 >= E) return;   // whole waves leave; the kernel has no barriers
-    const int ne = (int)(E - e0 < WD_Q ? E - e0 : WD_Q);
-    // lane L: sorted position e0 + L
-    uint32_t my_lab = 0xffffffffu, my_er = 0;
-    if (lane < ne) {
-        const uint32_t pe = perm[e0 + lane];
-        my_lab = elab[pe];
-        my_er = erow[pe];
-    }
-    const float *my_x = lane < ne ? wd_row(slices, nslices, d, my_er) : slices[0].X;
-    const uint64_t my_xa = (uint64_t)(uintptr_t)my_x;
-    const int W = d + 2;
-    const int64_t e1 = e0 + ne;
-    double acc[WD_MAXJ];
-#pragma unroll
-    for (int i = 0; i < WD_MAXJ; i++) acc[i] = 0.0;
-    double cntd = 0.0;
-    uint32_t cur = (uint32_t)__shfl((int)my_lab, 0);
-    auto flush = [&](uint32_t cl) {
-        const int64_t b = base[cl], e = b + counts[cl];
-        double *dst;
-        if (b >= e0 && e <= e1) {   // complete within the chunk
-            dst = tmp + (int64_t)cl * W;
-            if (lane == 0) {
-                dst[0] = cntd;
-                dst[1] = 0.0;
-            }
-            dst += 2;
-        } else {
-            dst = pieces + (q * 2 + (b <= e0 ? 0 : 1)) * (int64_t)(d + 1);
-            if (lane == 0) dst[d] = cntd;
-        }
-#pragma unroll
-        for (int i = 0; i < WD_MAXJ; i++) {
-            const int j = lane + 64 * i;
-            if (j < d) dst[j] = acc[i];
-            acc[i] = 0.0;
-        }
-        cntd = 0.0;
-    };
-    for (int t = 0; t < ne; t += 4) {
-        // the loads are unconditional (a lane past the last dim reads dim d - 1, a slot past the chunk's end reads
-        // row t again) and masked afterwards: guarded loads become one branch and one wait each
-        const gfloat *x[4];   // global address space: global loads, not flat ones
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            x[u] = (const gfloat *)(uintptr_t)(uint64_t)__shfl((long long)my_xa, t + u < ne ? t + u : t);
-        float v[4][WD_MAXJ];
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int i = 0; i < WD_MAXJ; i++) v[u][i] = x[u][min(lane + 64 * i, d - 1)];
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int i = 0; i < WD_MAXJ; i++)
-                if (t + u >= ne || lane + 64 * i >= d) v[u][i] = 0.0f;
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            if (t + u >= ne) break;
-            const uint32_t lb = (uint32_t)__shfl((int)my_lab, t + u);
-            const bool neg = ((uint32_t)__shfl((int)my_er, t + u) >> 31) != 0;
-            if (lb != cur) {
-                flush(cur);
-                cur = lb;
-            }
-#pragma unroll
-            for (int i = 0; i < WD_MAXJ; i++) acc[i] = neg ? acc[i] - (double)v[u][i] : acc[i] + (double)v[u][i];
-            cntd += neg ? -1.0 : 1.0;
-        }
-    }
-    flush(cur);
-}
-
-// Block per cluster: a cluster with no changed rows gets zero change; one whose run spans several chunks the sum
-// of its pieces in chunk order (the head slot of every chunk whose first position it holds, the tail slot of the
-// chunk it starts in otherwise); one inside a single chunk was written whole by that chunk's wave.
-__global__ __launch_bounds__(256) void k_wd_combine(const uint32_t *__restrict__ counts,
-                                                    const uint32_t *__restrict__ base, int d,
-                                                    const double *__restrict__ pieces, double *__restrict__ tmp,
-                                                    const int32_t *__restrict__ gate) {
-    if (*gate) return;
-    const int c = blockIdx.x, W = d + 2;
-    const int64_t cnt = counts[c], b = base[c];
-    double *dst = tmp + (int64_t)c * W;
-    if (cnt == 0) {
-        for (int j = threadIdx.x; j < W; j += 256) dst[j] = 0.0;
-        return;
-    }
-    const int64_t q0 = b / WD_Q, q1 = (b + cnt - 1) / WD_Q;
-    if (q0 == q1) return;
-    for (int j = threadIdx.x; j <= d; j += 256) {
-        double t = 0.0;
-        for (int64_t qa = q0; qa <= q1; qa += 8) {   // eight loads in flight, added in chunk order
-            double v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int64_t q = qa + u;
-                v[u] = q <= q1 ? pieces[(q * 2 + (b <= q * WD_Q ? 0 : 1)) * (int64_t)(d + 1) + j] : 0.0;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (qa + u <= q1) t += v[u];
-        }
-        if (j < d) dst[2 + j] = t;
-        else dst[0] = t;
-    }
-    if (threadIdx.x == 0) dst[1] = 0.0;
-}
-
 }  // namespace
 
 int64_t km_wd_blocks(int64_t n) { return (n + WD_RB - 1) / WD_RB; }
 int64_t km_wd_stat_blocks(int64_t n) { return (n + WD_SB - 1) / WD_SB; }
-int km_wd_max_dims() { return 64 * WD_MAXJ; }
+int km_wd_max_dims() { return KM_CHUNK_MAX_DIMS; }
 
 hipError_t km_launch_wd_stats(const km_slice *slices_h, const int64_t *rows, int nslices, int d, double *part,
                               double *mu_T, hipStream_t s) {
@@ -386,13 +244,11 @@ hipError_t km_launch_wd_gate(const uint32_t *lab, const uint32_t *prev, int64_t 
     return hipGetLastError();
 }
 
-int64_t km_wd_piece_doubles(int64_t limit, int d) { return (2 * limit + WD_Q - 1) / WD_Q * 2 * (int64_t)(d + 1); }
-
 hipError_t km_launch_wd_accum(const km_slice *slices_d, int nslices, int64_t n, int d, const uint32_t *lab,
                               const uint32_t *prev, int k, int64_t limit, const uint32_t *bcnt, uint32_t *elab,
                               uint32_t *erow, uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm,
                               double *pieces, double *tmp, const int32_t *gate, hipStream_t s) {
-    if (d < 1 || d > 64 * WD_MAXJ || n < 1 || n > (int64_t)0x7fffffff || nslices < 1 || limit < 1 || limit > n)
+    if (d < 1 || d > KM_CHUNK_MAX_DIMS || n < 1 || n > (int64_t)0x7fffffff || nslices < 1 || limit < 1 || limit > n)
         return hipErrorInvalidValue;
     const int nb = (int)km_wd_blocks(n);
     const int64_t len = 2 * limit;
@@ -403,10 +259,6 @@ hipError_t km_launch_wd_accum(const km_slice *slices_d, int nslices, int64_t n, 
                        bcnt + nb, (uint32_t)k, gate);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = km_launch_label_sort(elab, len, k + 1, H, counts, base, perm, gate, s)) != hipSuccess) return e;
-    const int64_t nq = (len + WD_Q - 1) / WD_Q;
-    hipLaunchKernelGGL(k_wd_chunks, dim3((unsigned)((nq + 3) / 4)), dim3(256), 0, s, slices_d, nslices, d, elab, erow,
-                       perm, counts, base, bcnt + nb, pieces, tmp, gate);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_wd_combine, dim3(k), dim3(256), 0, s, counts, base, d, pieces, tmp, gate);
-    return hipGetLastError();
+    return km_launch_chunk_sums(2, nullptr, slices_d, nslices, d, elab, erow, nullptr, nullptr, perm, counts, base, k,
+                                bcnt + nb, len, pieces, tmp, gate, s);
 }
