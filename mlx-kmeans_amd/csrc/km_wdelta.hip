@@ -76,22 +76,32 @@ __global__ __launch_bounds__(256) void k_wd_stats(const float *__restrict__ X, i
     if (threadIdx.x == 0) out[d] = red[0];
 }
 
-// mode 0: mu[j] = (the blocks' column sums in block order) / n; mode 1: mu[d] = T, the blocks' scatter in order.
+// mode 0 (a block per 64 dims): mu[j] = the blocks' column sums / n, each dim's sum taken as four interleaved
+// runs over the blocks added in run order; mode 1 (one block): mu[d] = T, the blocks' scatter as 256 interleaved
+// runs added by a fixed tree. Fixed orders: the same bits every time.
 __global__ __launch_bounds__(256) void k_wd_stats_fin(const double *__restrict__ part, int64_t nb, int d, int64_t n,
                                                       int mode, double *__restrict__ mu) {
+    __shared__ double red[256];
+    const int tid = threadIdx.x;
     if (mode) {
-        if (threadIdx.x == 0) {
-            double t = 0.0;
-            for (int64_t b = 0; b < nb; b++) t += part[b * (d + 1) + d];
-            mu[d] = t;
+        double t = 0.0;
+        for (int64_t b = tid; b < nb; b += 256) t += part[b * (d + 1) + d];
+        red[tid] = t;
+        __syncthreads();
+        for (int h = 128; h > 0; h >>= 1) {
+            if (tid < h) red[tid] += red[tid + h];
+            __syncthreads();
         }
+        if (tid == 0) mu[d] = red[0];
         return;
     }
-    for (int j = threadIdx.x; j < d; j += 256) {
-        double s = 0.0;
-        for (int64_t b = 0; b < nb; b++) s += part[b * (d + 1) + j];
-        mu[j] = s / (double)n;
-    }
+    const int j = blockIdx.x * 64 + (tid & 63), g = tid >> 6;
+    double sj = 0.0;
+    if (j < d)
+        for (int64_t b = g; b < nb; b += 4) sj += part[b * (d + 1) + j];
+    red[tid] = sj;
+    __syncthreads();
+    if (g == 0 && j < d) mu[j] = (((red[tid] + red[tid + 64]) + red[tid + 128]) + red[tid + 192]) / (double)n;
 }
 
 // Rows whose label changed, per block of WD_RB rows.
@@ -226,7 +236,7 @@ hipError_t km_launch_wd_stats(const km_slice *slices_h, const int64_t *rows, int
             if (e != hipSuccess) return e;
             b0 += nb;
         }
-        hipLaunchKernelGGL(k_wd_stats_fin, dim3(1), dim3(256), 0, s, part, nbt, d, n, mode, mu_T);
+        hipLaunchKernelGGL(k_wd_stats_fin, dim3(mode ? 1 : (d + 63) / 64), dim3(256), 0, s, part, nbt, d, n, mode, mu_T);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
