@@ -861,9 +861,7 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
     const int64_t slots = (int64_t)dev.cus * occ;
     const int64_t unit = 64 * waves;
     const int64_t units = (n + unit - 1) / unit;
-    // at least two units per block where there are fewer than two per slot: small inputs write half the per-block
-    // partials and the reduce reads half (100k x 32: 0.036 -> 0.033 ms per pass)
-    int64_t nrb = (units + 1) / 2 < slots ? (units + 1) / 2 : slots;
+    int64_t nrb = units < slots ? units : slots;
     if (max_blocks > 0 && nrb > max_blocks) nrb = max_blocks;
     if (nrb < 1) nrb = 1;
     pl.nrb = (int)nrb;
