@@ -101,7 +101,7 @@ struct km_ctx {
     // wlab (odd passes), each pass compared with the other
     DBuf<uint32_t> wlab;
     DBuf<uint32_t> wd_bcnt, wd_e;   // per-block change counts + m; the entry arrays (elab, erow: wd_limit each x2)
-    DBuf<uint32_t> wd_H, wd_cnt, wd_base, wd_perm;   // the entries' counting sort by label (k + 1 labels)
+    DBuf<uint32_t> wd_H, wd_cnt, wd_base, wd_perm;   // the entries' counting sort by label
     DBuf<int32_t> wd_gate;          // [0] nonzero: no change-only sums this pass; [1] nonzero: no full accumulation
     DBuf<double> wd_part, wd_mu;    // mean / scatter partials; [mu (d), T] of the data set
     DBuf<double> pieces;            // the sums of clusters whose sorted rows span several chunks, per chunk
@@ -818,10 +818,10 @@ static int queue_iteration(km_ctx *c, int k, int mode, int path, int pass, doubl
                     KM_FIN_UPDATE | (spherical ? KM_FIN_SPHERICAL : 0), lmode);
 }
 
-// The most changed rows a pass of the wide-row path takes as change-only sums: they sort 2 limit entries and read
-// each changed row twice, the full accumulation sorts and reads every row once; a quarter of the rows leaves the
-// change-only sums the cheaper at every shape.
-static int64_t wide_delta_limit(int64_t n) { return n / 4; }
+// The most changed rows a pass of the wide-row path takes as change-only sums: they sort 2m entries and read each
+// changed row twice, the full accumulation sorts and reads every row once; below half the rows the change-only
+// sums are the cheaper.
+static int64_t wide_delta_limit(int64_t n) { return n / 2; }
 
 // The wide-row path's change-only accumulation: the second label array, the count and entry arrays, and once per
 // data set the slice table and [mu, T] (queued on the stream before the loop's first pass).
@@ -836,9 +836,9 @@ static int prepare_wide_delta(km_ctx *c, int k, bool *use) {
     HIPCHK(c, c->wlab.ensure((size_t)c->n));
     HIPCHK(c, c->wd_bcnt.ensure((size_t)km_wd_blocks(c->n) + 1));
     HIPCHK(c, c->wd_e.ensure((size_t)limit * 4));
-    HIPCHK(c, c->wd_H.ensure((size_t)km_sorted_blocks(2 * limit) * (k + 1)));
-    HIPCHK(c, c->wd_cnt.ensure((size_t)k + 1));
-    HIPCHK(c, c->wd_base.ensure((size_t)k + 1));
+    HIPCHK(c, c->wd_H.ensure((size_t)km_sorted_blocks(2 * limit) * k));
+    HIPCHK(c, c->wd_cnt.ensure((size_t)k));
+    HIPCHK(c, c->wd_base.ensure((size_t)k));
     HIPCHK(c, c->wd_perm.ensure((size_t)limit * 2));
     int64_t max_rows = 0;
     for (auto &p : c->parts) max_rows = std::max(max_rows, p.rows);

@@ -812,9 +812,19 @@ __global__ __launch_bounds__(256) void k_big_fkeys_fin(const uint64_t *__restric
 
 static constexpr int KB_RB = 4096;   // rows per histogram / scatter block
 
+// half (may be null): the sort takes only the first 2 *half of the n labels (a count known on the device); blocks
+// past them write zero counts.
+__device__ __forceinline__ int64_t kb_sort_len(int64_t n, const uint32_t *half) {
+    if (!half) return n;
+    const int64_t m = 2 * (int64_t)*half;
+    return m < n ? m : n;
+}
+
 __global__ __launch_bounds__(256) void k_big_hist(const uint32_t *__restrict__ labels, int64_t n, int k,
-                                                  uint32_t *__restrict__ H, const int32_t *__restrict__ stop) {
+                                                  uint32_t *__restrict__ H, const uint32_t *__restrict__ half,
+                                                  const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
+    n = kb_sort_len(n, half);
     extern __shared__ uint32_t cnt[];
     for (int c = threadIdx.x; c < k; c += 256) cnt[c] = 0;
     __syncthreads();
@@ -827,8 +837,10 @@ __global__ __launch_bounds__(256) void k_big_hist(const uint32_t *__restrict__ l
 
 // The same histogram with the counters in global memory (H zeroed first), for k too large for LDS.
 __global__ __launch_bounds__(256) void k_big_hist_g(const uint32_t *__restrict__ labels, int64_t n, int k,
-                                                    uint32_t *__restrict__ H, const int32_t *__restrict__ stop) {
+                                                    uint32_t *__restrict__ H, const uint32_t *__restrict__ half,
+                                                    const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
+    n = kb_sort_len(n, half);
     const int64_t r0 = (int64_t)blockIdx.x * KB_RB;
     const int64_t r1 = (r0 + KB_RB < n) ? r0 + KB_RB : n;
     for (int64_t r = r0 + threadIdx.x; r < r1; r += 256) atomicAdd(&H[(int64_t)blockIdx.x * k + labels[r]], 1u);
@@ -930,8 +942,11 @@ __device__ __forceinline__ void kb_scatter_body(const uint32_t *__restrict__ lab
 __global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict__ labels, int64_t n, int k,
                                                      int nbits, const uint32_t *__restrict__ O,
                                                      const uint32_t *__restrict__ base, uint32_t *__restrict__ perm,
+                                                     const uint32_t *__restrict__ half,
                                                      const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
+    n = kb_sort_len(n, half);
+    if ((int64_t)blockIdx.x * KB_RB >= n) return;   // block-uniform: no rows, no barriers
     extern __shared__ uint32_t run[];   // k running offsets
     for (int c = threadIdx.x; c < k; c += 256) run[c] = base[c] + O[(int64_t)blockIdx.x * k + c];
     kb_scatter_body<false>(labels, n, nbits, run, base, perm);
@@ -942,8 +957,10 @@ __global__ __launch_bounds__(256) void k_big_scatter(const uint32_t *__restrict_
 __global__ __launch_bounds__(256) void k_big_scatter_g(const uint32_t *__restrict__ labels, int64_t n, int k,
                                                        int nbits, uint32_t *__restrict__ O,
                                                        const uint32_t *__restrict__ base, uint32_t *__restrict__ perm,
+                                                       const uint32_t *__restrict__ half,
                                                        const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
+    n = kb_sort_len(n, half);
     kb_scatter_body<true>(labels, n, nbits, O + (int64_t)blockIdx.x * k, base, perm);
 }
 
@@ -1094,7 +1111,8 @@ hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32
 }
 
 hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32_t *H, uint32_t *counts,
-                                uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s) {
+                                uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s,
+                                const uint32_t *half) {
     // counters in LDS up to KM_BIG_PACK_MAX_K labels (16 KB), in global memory above
     const bool glob = k > KM_BIG_PACK_MAX_K;
     const int nb = (int)km_sorted_blocks(n);
@@ -1104,9 +1122,9 @@ hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32
         hipLaunchKernelGGL(k_big_zero, dim3((unsigned)std::min<int64_t>((cells + 255) / 256, 4096)), dim3(256), 0, s, H,
                            cells, stop);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL(k_big_hist_g, dim3(nb), dim3(256), 0, s, labels, n, k, H, stop);
+        hipLaunchKernelGGL(k_big_hist_g, dim3(nb), dim3(256), 0, s, labels, n, k, H, half, stop);
     } else {
-        hipLaunchKernelGGL(k_big_hist, dim3(nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, stop);
+        hipLaunchKernelGGL(k_big_hist, dim3(nb), dim3(256), (size_t)k * 4, s, labels, n, k, H, half, stop);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_big_scan, dim3(1), dim3(1024), 0, s, H, nb, k, counts, base, stop);
@@ -1114,10 +1132,11 @@ hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32
     int nbits = 1;   // bits of the largest label, k - 1
     while (nbits < 32 && ((uint32_t)(k - 1) >> nbits) != 0u) nbits++;
     if (glob)
-        hipLaunchKernelGGL(k_big_scatter_g, dim3(nb), dim3(256), 0, s, labels, n, k, nbits, H, base, perm, stop);
+        hipLaunchKernelGGL(k_big_scatter_g, dim3(nb), dim3(256), 0, s, labels, n, k, nbits, H, base, perm, half,
+                           stop);
     else
         hipLaunchKernelGGL(k_big_scatter, dim3(nb), dim3(256), (size_t)k * 4, s, labels, n, k, nbits, H, base, perm,
-                           stop);
+                           half, stop);
     return hipGetLastError();
 }
 

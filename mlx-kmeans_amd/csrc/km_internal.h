@@ -121,8 +121,8 @@ hipError_t km_launch_wd_stats(const km_slice *slices_h, const int64_t *rows, int
 hipError_t km_launch_wd_gate(const uint32_t *lab, const uint32_t *prev, int64_t n, int64_t limit, uint32_t *bcnt,
                              int32_t *gate, const int32_t *stop, hipStream_t s);
 // The change sums into tmp (k (d + 2), column 1 zero) when gate[0] is 0. elab, erow and perm hold 2 limit words
-// each, H km_sorted_blocks(2 limit) x (k + 1) counters, counts / base k + 1 words, pieces
-// km_chunk_piece_doubles(2 limit, d, 2); slices_d a device copy of the slice table
+// each, H km_sorted_blocks(2 limit) x k counters, counts / base k words, pieces km_chunk_piece_doubles(2 limit, d,
+// 2); slices_d a device copy of the slice table
 hipError_t km_launch_wd_accum(const km_slice *slices_d, int nslices, int64_t n, int d, const uint32_t *lab,
                               const uint32_t *prev, int k, int64_t limit, const uint32_t *bcnt, uint32_t *elab,
                               uint32_t *erow, uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm,
@@ -259,9 +259,11 @@ hipError_t km_launch_chunk_sums(int mode, const float *X, const km_slice *slices
 // labels and best are known. H holds km_sorted_blocks(n) x k counters; tmp receives the k (d + 2) range sums.
 int64_t km_sorted_blocks(int64_t n);
 // The stable counting sort by label alone: perm lists 0 .. n-1 grouped by label (ascending), ascending within a
-// label; counts / base the k group sizes and starts. H holds km_sorted_blocks(n) x k counters.
+// label; counts / base the k group sizes and starts. H holds km_sorted_blocks(n) x k counters. half (device, may
+// be null): sort only the first 2 *half labels.
 hipError_t km_launch_label_sort(const uint32_t *labels, int64_t n, int k, uint32_t *H, uint32_t *counts,
-                                uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s);
+                                uint32_t *base, uint32_t *perm, const int32_t *stop, hipStream_t s,
+                                const uint32_t *half = nullptr);
 hipError_t km_launch_sorted_accum(const float *X, int64_t n, int d, const uint32_t *labels, const float *best, int k,
                                   uint32_t *H, uint32_t *counts, uint32_t *base, uint32_t *perm, double *pieces,
                                   double *tmp, const int32_t *stop, hipStream_t s);

@@ -203,15 +203,6 @@ __global__ __launch_bounds__(256) void k_wd_write(const uint32_t *__restrict__ l
     }
 }
 
-// Entries 2m .. 2 limit - 1 take the label k, which no cluster block reads: the sort then runs over a size the
-// host knows.
-__global__ __launch_bounds__(256) void k_wd_pad(uint32_t *__restrict__ elab, int64_t len, const uint32_t *__restrict__ mcount,
-                                                uint32_t k, const int32_t *__restrict__ gate) {
-    if (*gate) return;
-    const int64_t e0 = 2 * (int64_t)*mcount;
-    for (int64_t e = e0 + (int64_t)blockIdx.x * 256 + threadIdx.x; e < len; e += (int64_t)gridDim.x * 256) elab[e] = k;
-}
-
 }  // namespace
 
 int64_t km_wd_blocks(int64_t n) { return (n + WD_RB - 1) / WD_RB; }
@@ -265,10 +256,8 @@ hipError_t km_launch_wd_accum(const km_slice *slices_d, int nslices, int64_t n, 
     hipLaunchKernelGGL(k_wd_write, dim3(nb), dim3(256), 0, s, lab, prev, n, bcnt, nb, elab, erow, gate);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_wd_pad, dim3((unsigned)std::min<int64_t>((len + 255) / 256, 2048)), dim3(256), 0, s, elab, len,
-                       bcnt + nb, (uint32_t)k, gate);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = km_launch_label_sort(elab, len, k + 1, H, counts, base, perm, gate, s)) != hipSuccess) return e;
+    // the sort takes the 2m entries written (m on the device), not the 2 limit the arrays hold
+    if ((e = km_launch_label_sort(elab, len, k, H, counts, base, perm, gate, s, bcnt + nb)) != hipSuccess) return e;
     return km_launch_chunk_sums(2, nullptr, slices_d, nslices, d, elab, erow, nullptr, nullptr, perm, counts, base, k,
                                 bcnt + nb, len, pieces, tmp, gate, s);
 }
