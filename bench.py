@@ -255,7 +255,7 @@ def main():
                            "passes": int(len(pass_ms)),
                            "note": "HIP events at every pass boundary of a second timed loop; the first pass of "
                                    "a fit accumulates every row, later passes only the rows whose label changed "
-                                   "(on the wide-row path, when at most a quarter of the rows changed)"},
+                                   "(on the wide-row path, when at most half the rows changed)"},
         "stream_read_gbs": round(stream_gbs, 1),
         "final_inertia": inertia,
         "roofline": roof,
