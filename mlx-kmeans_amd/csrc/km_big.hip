@@ -623,9 +623,18 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                 const float *xr = xs + ir * (KB_RCH + 1);
                 const float *cc = cs + tid * (KB_RCH + 1);
                 float sv = sacc;
-                for (int jj = 0; jj < w; jj++) {
-                    const float t = xr[jj] - cc[jj];
-                    sv = sv + t * t;
+                // a whole chunk unrolled: its LDS reads issue ahead of the dependent sum (dims still ascending)
+                if (w == KB_RCH) {
+#pragma unroll
+                    for (int jj = 0; jj < KB_RCH; jj++) {
+                        const float t = xr[jj] - cc[jj];
+                        sv = sv + t * t;
+                    }
+                } else {
+                    for (int jj = 0; jj < w; jj++) {
+                        const float t = xr[jj] - cc[jj];
+                        sv = sv + t * t;
+                    }
                 }
                 sacc = sv;
             }
