@@ -13,11 +13,17 @@ typedef __attribute__((address_space(1))) void *gbl_vptr;
 // the current block, which drained the double buffer at every step.) M0 holds the
 // wave-uniform LDS address and needs one wait state before the load reads it. M0 is a register the compiler
 // reserves (it sets it before each of its own uses), so naming it as clobbered is harmless and only warned about.
+// NT: the non-temporal hint, for data a pass reads once (the rows, the per-row label state): on MI355X a plain
+// streaming read reaches 7.0-7.1 TB/s with it and 6.2-6.3 without.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(const void *src, lds_vptr dst) {
     const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+    if constexpr (NT)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(m) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 

@@ -210,13 +210,14 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8 &ph, bf16x8 &
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// Rows reach LDS by direct global->LDS loads (global_load_lds_dwordx4), double-buffered one 64-row block
-// ahead. A block is its 64 rows in order (D floats = NC 16-byte chunks each); one load instruction moves 1 KB, i.e.
-// 64/NC whole rows read contiguously, lane i taking the 16 bytes that land at LDS offset 16 i. Within each row the
-// chunks are permuted (chunk c of block row r sits at position c ^ swz(r)) so that the screen's half-row reads
-// (eight lanes on eight consecutive rows, one chunk each) and the accumulation's transposed reads (one dim per
-// lane, one row per read) touch distinct LDS banks (32 banks of 4 bytes). swz depends only on the row's low bits,
-// which are compile-time in the transposed reads, so their addresses stay a few registers plus immediates.
+// Rows reach LDS by direct global->LDS loads (global_load_lds_dwordx4, non-temporal: a pass reads each row once),
+// double-buffered one 64-row block ahead. A block is its 64 rows in order (D floats = NC 16-byte chunks each); one
+// load instruction moves 1 KB, i.e. 64/NC whole rows read contiguously, lane i taking the 16 bytes that land at LDS
+// offset 16 i. Within each row the chunks are permuted (chunk c of block row r sits at position c ^ swz(r)) so
+// that the screen's half-row reads (eight lanes on eight consecutive rows, one chunk each) and the accumulation's
+// transposed reads (one dim per lane, one row per read) touch distinct LDS banks (32 banks of 4 bytes). swz
+// depends only on the row's low bits, which are compile-time in the transposed reads, so their addresses stay a
+// few registers plus immediates.
 template <int D>
 struct Lay {
     static constexpr int NC = D / 4;           // 16-byte chunks per row
@@ -248,7 +249,7 @@ __device__ __forceinline__ void issue_block(const float *__restrict__ X, int64_t
         int64_t row = r0 + r;
         row = row < r_end ? row : r_end - 1;
         const float *src = X + row * D + 4 * (p ^ swz<D>(r));
-        lds_dma16(src, (lds_vptr)(buf + q * 1024));
+        lds_dma16<true>(src, (lds_vptr)(buf + q * 1024));
     }
 }
 
@@ -262,7 +263,7 @@ template <int D, int Q>
 __device__ __forceinline__ void issue_block_inner(const char *blk, uint32_t voff0, uint32_t voff1, uint32_t mb) {
     if constexpr (Q < Lay<D>::NC) {
         const char *sb = blk + (Q / 4) * 4096;   // the immediate offset reaches 4095
-        asm volatile("s_add_u32 m0, %1, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2 offset:%3"
+        asm volatile("s_add_u32 m0, %1, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2 offset:%3 nt"
                      ::"v"((Q & 1) ? voff1 : voff0), "s"(mb), "s"(sb), "n"((Q % 4) * 1024), "n"((Q / 4) * 4096)
                      : "memory", "m0", "scc");
         issue_block_inner<D, Q + 1>(blk, voff0, voff1, mb);
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(64 * WAVES, D >= 64 ? 1 : 2) void k_fused_mfma(
     const uint32_t voff0 = issue_voff<D>(lane, 0), voff1 = issue_voff<D>(lane, 1);
     if (r0 + 64 <= r_end) issue_block_inner_all<D>(X + r0 * D, voff0, voff1, wbase);
     else if (r0 < r_end) issue_block<D>(X, r0, r_end, lane, wbase);
-    if (LM == 2 && r0 < r_end && lane < 4) lds_dma16(lprev + r0 + 16 * lane, (lds_vptr)(wbase + L::BUF));
+    if (LM == 2 && r0 < r_end && lane < 4) lds_dma16<true>(lprev + r0 + 16 * lane, (lds_vptr)(wbase + L::BUF));
 
     for (int e = threadIdx.x; e < KP * CS; e += 64 * WAVES) {
         const int c = e / CS, j = e % CS;
@@ -448,7 +449,7 @@ __global__ __launch_bounds__(64 * WAVES, D >= 64 ? 1 : 2) void k_fused_mfma(
         if (r1 < r_end) {
             if (r1 + 64 <= r_end) issue_block_inner_all<D>(X + r1 * D, voff0, voff1, wbase + (cur ^ LB));
             else issue_block<D>(X, r1, r_end, lane, wbase + (cur ^ LB));
-            if (LM == 2 && lane < 4) lds_dma16(lprev + r1 + 16 * lane, (lds_vptr)(wbase + (cur ^ LB) + L::BUF));
+            if (LM == 2 && lane < 4) lds_dma16<true>(lprev + r1 + 16 * lane, (lds_vptr)(wbase + (cur ^ LB) + L::BUF));
             vm_wait<L::NC + LX>();
         } else {
             vm_wait<0>();
