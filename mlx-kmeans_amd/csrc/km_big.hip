@@ -31,6 +31,7 @@
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float kb_f4 __attribute__((ext_vector_type(4)));
 
 static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
 static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
@@ -564,7 +565,10 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                 for (int u = 0; u < XPT / 4; u++) {
                     const int r = tid / 8 + 32 * u, p = tid % 8;
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (r < nr && 4 * p < w) v = *reinterpret_cast<const float4 *>(X + (int64_t)rid[r] * d + j0 + 4 * p);
+                    if (r < nr && 4 * p < w) {   // each listed row once per pass: non-temporal
+                        const kb_f4 q = __builtin_nontemporal_load(reinterpret_cast<const kb_f4 *>(X + (int64_t)rid[r] * d + j0 + 4 * p));
+                        v = make_float4(q.x, q.y, q.z, q.w);
+                    }
                     xv[4 * u] = v.x;
                     xv[4 * u + 1] = v.y;
                     xv[4 * u + 2] = v.z;

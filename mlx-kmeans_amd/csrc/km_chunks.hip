@@ -124,7 +124,10 @@ __global__ __launch_bounds__(256) void k_chunk_sums(const float *__restrict__ X,
 #pragma unroll
             for (int u = 0; u < 4; u++)
 #pragma unroll
-                for (int i = 0; i < NJ; i++) v[u][i] = x[u][min(lane + 64 * i, d - 1)];
+                for (int i = 0; i < NJ; i++) {   // the full accumulation reads each row once: non-temporal
+                    const gfloat *a = &x[u][min(lane + 64 * i, d - 1)];
+                    v[u][i] = MODE == 2 ? *a : __builtin_nontemporal_load(a);
+                }
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 if (t + u >= ns) break;   // wave-uniform
