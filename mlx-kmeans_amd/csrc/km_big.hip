@@ -32,6 +32,7 @@
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float kb_f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int kb_u4 __attribute__((ext_vector_type(4)));
 
 static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
 static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
@@ -276,8 +277,9 @@ __global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
     bf16x8 B[DS];
 #pragma unroll
     for (int s = 0; s < DS; s++) {
-        if (have) {
-            const uint4 v = *reinterpret_cast<const uint4 *>(X16T + ((tile * DS + s) * 64 + lane) * 8);
+        if (have) {   // each row once per pass: non-temporal
+            const kb_u4 q = __builtin_nontemporal_load(reinterpret_cast<const kb_u4 *>(X16T + ((tile * DS + s) * 64 + lane) * 8));
+            const uint4 v = make_uint4(q.x, q.y, q.z, q.w);
             B[s] = *reinterpret_cast<const bf16x8 *>(&v);
         } else {
             B[s] = bf16x8{};
