@@ -1,4 +1,4 @@
-// Exact Lloyd pass for wide rows (16 < dims <= 768, k <= 65536): the reference's "tiles" design (core.py:616-651,
+// Exact Lloyd pass for wide rows (16 < dims <= 1536, k <= 65536): the reference's "tiles" design (core.py:616-651,
 // 310-377: matrix-unit dot products, an error margin, exact rescoring of the candidates) rebuilt for CDNA4, plus
 // its sorted accumulation (core.py:934-994, 424-449, 1421-1441).
 //
@@ -246,8 +246,11 @@ __global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C
 // window, and at the end keeps the listed centres inside the final window - exactly the centres the final window
 // admits. A half-row with more than KB_HALF of them at once (or non-finite data) sends the row to a full scan.
 
+// The wave's 32 rows stay in registers as B operands (4 per K-step): up to 48 K-steps two blocks share a CU (256
+// registers a wave); above that one block does, and the 512 registers of a lone wave per SIMD (accumulation
+// registers included, which the matrix cores read operands from) hold up to 96 K-steps without spilling.
 template <int DS, bool PACK>
-__global__ __launch_bounds__(64 * KB_WAVES, 2) void k_big_screen(
+__global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
     const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
     int approx, const uint32_t *__restrict__ xmax, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand,
@@ -995,13 +998,15 @@ static screen_fn kb_screen_for(int DS) {
         case 24: return k_big_screen<24, PACK>;
         case 32: return k_big_screen<32, PACK>;
         case 48: return k_big_screen<48, PACK>;
+        case 64: return k_big_screen<64, PACK>;
+        case 96: return k_big_screen<96, PACK>;
         default: return nullptr;
     }
 }
 
 static int kb_ds(int d) {
     const int s = (d + 15) / 16;
-    const int opts[] = {2, 4, 8, 16, 24, 32, 48};
+    const int opts[] = {2, 4, 8, 16, 24, 32, 48, 64, 96};
     for (int o : opts)
         if (s <= o) return o;
     return 0;
@@ -1009,7 +1014,7 @@ static int kb_ds(int d) {
 
 km_big_plan km_plan_big(int64_t n, int d, int k) {
     km_big_plan pl{};
-    if (d <= 16 || d > 768 || k < 1 || k > KM_BIG_MAX_K || n < 1) return pl;
+    if (d <= 16 || d > KM_BIG_MAX_DIMS || k < 1 || k > KM_BIG_MAX_K || n < 1) return pl;
     pl.ok = 1;
     pl.DS = kb_ds(d);
     pl.kpad = (k + 31) / 32 * 32;

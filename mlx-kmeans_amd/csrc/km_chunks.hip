@@ -223,6 +223,11 @@ chunk_fn chunk_for(int nj) {
         case 11: return k_chunk_sums<11, MODE>;
         case 12: return k_chunk_sums<12, MODE>;
         case 13: return k_chunk_sums<13, MODE>;
+        case 14: return k_chunk_sums<14, MODE>;
+        case 15: return k_chunk_sums<15, MODE>;
+        case 16: return k_chunk_sums<16, MODE>;
+        case 20: return k_chunk_sums<20, MODE>;
+        case 24: return k_chunk_sums<24, MODE>;
         default: return nullptr;
     }
 }
@@ -241,7 +246,9 @@ hipError_t km_launch_chunk_sums(int mode, const float *X, const km_slice *slices
     if (d < 1 || d > KM_CHUNK_MAX_DIMS || npos < 1 || mode < 0 || mode > 2 || k < 1 ||
         (mode == 2 ? (!slices || nslices < 1) : !X))
         return hipErrorInvalidValue;
-    const int nj = (d + 63) / 64;
+    // dims per lane: ceil(d / 64), above 16 rounded up to 20 or 24 (the lanes past the last dim add zeros)
+    int nj = (d + 63) / 64;
+    if (nj > 16) nj = nj <= 20 ? 20 : 24;
     const chunk_fn fn = mode == 0 ? chunk_for<0>(nj) : mode == 1 ? chunk_for<1>(nj) : chunk_for<2>(nj);
     if (!fn) return hipErrorInvalidValue;
     const int Q = mode == 2 ? kc_q<2>() : kc_q<0>();

@@ -192,7 +192,8 @@ hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s);
 
-// Wide rows (16 < dims <= 768, k <= 4096): bf16 MFMA screen keeping 8 keys per row, exact rescoring of the
+// Wide rows (16 < dims <= KM_BIG_MAX_DIMS, k <= KM_BIG_MAX_K): bf16 MFMA screen keeping up to 16 keys per half-row,
+// exact rescoring of the
 // candidates, stable counting sort by label and per-cluster float64 sums.
 struct km_big_plan {
     int ok;
@@ -207,6 +208,8 @@ struct km_big_plan {
 // 2^-11 at most); above it, up to KM_BIG_MAX_K, the screen keeps each listed key's index beside it.
 #define KM_BIG_PACK_MAX_K 4096
 #define KM_BIG_MAX_K 65536   // centre indices are uint16 (0 .. 65535)
+// Widest rows the screen serves: 96 K-steps of 16 dims, the wave's 32 rows held as MFMA operands in registers
+#define KM_BIG_MAX_DIMS 1536
 km_big_plan km_plan_big(int64_t n, int d, int k);
 size_t km_big_x16_elems(const km_big_plan &pl);   // uint16 elements of the bf16 row operands
 size_t km_big_cop_elems(const km_big_plan &pl);   // uint16 elements of the bf16 centre operands
@@ -248,7 +251,7 @@ hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n,
                                uint32_t *base, uint32_t *perm, double *pieces, double *tmp, const int32_t *stop,
                                hipStream_t s);
 // ---- per-cluster sums over rows listed in cluster order, in fixed chunks (km_chunks.hip)
-#define KM_CHUNK_MAX_DIMS 832
+#define KM_CHUNK_MAX_DIMS 1536
 // pieces for npos listed positions: mode 0 (rows, best[] column) and 1 (rows, distances to C), mode 2 (change
 // entries)
 int64_t km_chunk_piece_doubles(int64_t npos, int d, int mode);
@@ -261,7 +264,7 @@ hipError_t km_launch_chunk_sums(int mode, const float *X, const km_slice *slices
                                 const uint32_t *perm, const uint32_t *counts, const uint32_t *base, int k,
                                 const uint32_t *npos_dev, int64_t npos, double *pieces, double *tmp,
                                 const int32_t *gate, hipStream_t s);
-// The counting sort by label and per-cluster float64 sums in row order for any rows path (d < 832): rows whose
+// The counting sort by label and per-cluster float64 sums in row order for any rows path (d <= 1536): rows whose
 // labels and best are known. H holds km_sorted_blocks(n) x k counters; tmp receives the k (d + 2) range sums.
 int64_t km_sorted_blocks(int64_t n);
 // The stable counting sort by label alone: perm lists 0 .. n-1 grouped by label (ascending), ascending within a

@@ -1,5 +1,5 @@
 """GPU: degenerate shapes on every path that serves them - a single row, a single centre, fewer rows than one
-64-row block, as many centres as rows (every row its own centre: distance 0), a few wide rows. Labels and best are
+64-row block, as many centres as rows (every row its own centre: distance 0), a few wide rows (768 to 1536 dims). Labels and best are
 the oracle's rows loop (core.py:263-274) bit for bit, the totals agree with the oracle's, and a Lloyd step and a
 fit with one centre end at the rows' mean (the reference's KMeans accepts n_clusters=1, estimator.py:7-230)."""
 import numpy as np
@@ -23,14 +23,14 @@ def lib():
 
 def served(path, d, k):
     if path == "mfma":    # the fused screen (d = 16, 32 with k <= 64; d = 64 with k <= 32) or the wide-row screen
-        return d in (16, 32) and k <= 64 or d == 64 and k <= 32 or 16 < d <= 768 and k <= 4096
+        return d in (16, 32) and k <= 64 or d == 64 and k <= 32 or 16 < d <= 1536 and k <= 4096
     if path == "fused":   # the low-d single-read path: d <= 16, k (d + 2) <= 768
         return d <= 16 and k * (d + 2) <= 768
     return True
 
 
 CASES = [(1, 3, 1), (5, 4, 1), (63, 16, 1), (65, 32, 2), (48, 32, 48), (64, 8, 64), (7, 48, 3), (40, 768, 2),
-         (100, 32, 100)]
+         (100, 32, 100), (3, 1536, 2), (33, 1000, 33)]
 
 
 @pytest.mark.parametrize("n,d,k", CASES)

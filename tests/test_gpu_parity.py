@@ -34,8 +34,8 @@ def lib():
 
 def mfma_served(d, k):
     """The fused screen serves d = 16, 32 with k <= 64 and d = 64 with k <= 32; the wide-row screen serves
-    16 < d <= 768 with k <= 4096."""
-    return d in (16, 32) and k <= 64 or d == 64 and k <= 32 or 16 < d <= 768 and k <= 4096
+    16 < d <= 1536 with k <= 4096."""
+    return d in (16, 32) and k <= 64 or d == 64 and k <= 32 or 16 < d <= 1536 and k <= 4096
 
 
 def fused_served(d, k):

@@ -1,0 +1,104 @@
+"""GPU: rows of 769 to 1536 dims on the wide-row path (GIST-like 960-dim descriptors, 1024- and 1536-dim
+embeddings), the reference's tiles design (core.py:616-651, 310-377) at the widths its tiles path takes.
+
+From 49 K-steps of 16 dims the screen runs one block per CU (its 32 rows per wave held as matrix-core operands in
+up to 384 registers) and the per-cluster sums take 14 to 24 dims per lane. Labels and best must be the rows loop's
+(core.py:263-274) bit for bit against the oracle on every row, on every path that serves the shape; the totals
+within the reference's accuracy bar (tests/accuracy.py:91-99); one Lloyd step against the oracle's; and a fit loop
+whose passes take the change-only sums must reach the centres that single steps with full sums reach.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+CENTRE_TOL = 1e-6
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mlx_kmeans import _lib
+    _lib.lib()
+    return _lib
+
+
+def _blobs(seed, n, d, k, true_k, parts=1):
+    rng = np.random.default_rng(seed)
+    cen = rng.uniform(-1, 1, (true_k, d)).astype(np.float32)
+    X = (cen[rng.integers(0, true_k, n)] + 0.35 * rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(n, k, replace=False)].copy()
+    cuts = np.linspace(0, n, parts + 1).astype(int)
+    return X, C, [X[cuts[i]:cuts[i + 1]] for i in range(parts)]
+
+
+@pytest.mark.parametrize("n,d,k,parts", [(20_000, 960, 304, 1), (10_007, 1000, 100, 2), (8_000, 1536, 64, 1),
+                                         (6_001, 1100, 257, 3), (30_000, 1024, 1024, 1), (5_000, 770, 33, 1),
+                                         (6_000, 1040, 4500, 1)])
+def test_wide_rows_match_the_oracle(lib, n, d, k, parts):
+    import oracle
+    X, C, slices = _blobs(n + d + k, n, d, k, max(k // 4, 3), parts)
+    ol, ob = oracle.assign(X, C)
+    ot = oracle.totals(X, ol, ob, k)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(slices)
+    for path in ("auto", "mfma", "rows"):
+        say(f"[gpu] wide rows n={n} d={d} k={k} parts={parts} path={path}")
+        tot, labels, best = ctx.run_pass(C, path=lib.PATHS[path], labels=True, best=True)
+        assert ctx.last_path() == ("rows" if path == "rows" else "mfma")
+        assert np.array_equal(labels, ol), (path, np.flatnonzero(labels != ol)[:10])
+        assert np.array_equal(best.view(np.uint32), ob.view(np.uint32)), path
+        counts = np.rint(tot[:, 0]).astype(np.int64)
+        assert np.array_equal(counts, np.rint(ot[:, 0]).astype(np.int64)), path
+        used = counts > 0
+        err = float(np.max(np.abs(tot[used, 2:] - ot[used, 2:]) / counts[used, None])) / scale
+        assert err <= CENTRE_TOL, (path, err)
+        ri = float(ot[:, 1].sum())
+        assert abs(float(tot[:, 1].sum()) - ri) <= 1e-6 * ri, path
+    say(f"[gpu]   rows scored against every centre: {ctx.fallback_rows()}")
+    C1, inertia, n_empty = ctx.lloyd_step(C)
+    R1, r_in, r_empty, _, _, _ = oracle.lloyd_step(X, C)
+    assert n_empty == r_empty
+    assert abs(inertia - r_in) <= 1e-6 * r_in
+    assert float(np.max(np.abs(C1.astype(np.float64) - R1))) / scale <= CENTRE_TOL
+    ctx.close()
+
+
+@pytest.mark.parametrize("d,k,parts", [(960, 48, 1), (1536, 24, 2)])
+def test_wide_rows_fit_loop_matches_single_steps(lib, d, k, parts):
+    """km_fit's passes after the first add only the rows that changed cluster when at most half of them did, and
+    the full sums otherwise; twelve passes must reach the centres (within 1e-6 of the RMS) and inertia (1e-6) of
+    twelve single Lloyd steps with full sums, and a rerun the same bits. The start is drawn from one corner of the
+    data, so that both kinds of pass occur."""
+    rng = np.random.default_rng(77 + d + k)
+    n = 60_013
+    cen = rng.uniform(-1, 1, size=(k, d)).astype(np.float32)
+    X = (cen[rng.integers(0, k, n)] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    order = np.argsort(X[:, 0])
+    C0 = X[order[rng.choice(n // 20, k, replace=False)]].copy()
+    cuts = np.linspace(0, n, parts + 1).astype(int)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts([X[cuts[i]:cuts[i + 1]] for i in range(parts)])
+    steps = 12
+    say(f"[gpu] wide fit loop d={d} k={k} parts={parts}")
+    C_fit, in_fit, it_fit, _ = ctx.fit(C0, steps, -1.0)
+    assert it_fit == steps and ctx.last_path() == "mfma"
+    C, moved, prev = C0, [], None
+    for _ in range(steps):
+        _, lab, _ = ctx.run_pass(C, labels=True)
+        if prev is not None:
+            moved.append(int((lab != prev).sum()))
+        prev = lab
+        C, inertia, _ = ctx.lloyd_step(C)
+    say(f"[gpu]   rows changing cluster per pass: {moved}")
+    assert any(0 < m <= n // 2 for m in moved), "some pass should take the change-only sums"
+    assert float(np.max(np.abs(C_fit.astype(np.float64) - C.astype(np.float64)))) / scale <= CENTRE_TOL
+    assert abs(in_fit - inertia) <= 1e-6 * inertia
+    C2, in2, _, _ = ctx.fit(C0, steps, -1.0)
+    assert np.array_equal(C2, C_fit) and in2 == in_fit
+    ctx.close()
