@@ -14,7 +14,7 @@
  * s = sum_j (x_j - c_j)^2, accumulated for j ascending with the product and the add rounded separately,
  * lowest index on an exact tie (the rows loop, core.py:263-274); best is that s. Whatever kernel path runs,
  * the labels and best values are these, bit for bit. Mode KM_APPROX (exact=False, estimator.py:18-30): on the
- * wide-row path (16 < dims <= 768, k <= 4096, k * dims >= 1024) the label is the bf16 screen's minimiser, taken on
+ * wide-row path (16 < dims <= 1536, k <= 4096, k * dims >= 1024) the label is the bf16 screen's minimiser, taken on
  * trust, and best is the exact distance above to that label; every other path is exact in either mode.
  */
 #ifndef KMEANS_HIP_H
@@ -115,8 +115,8 @@ int32_t km_seed_pp(km_ctx *ctx, int32_t k, const int64_t *sample, int64_t m, int
  * returns without waiting. It allocates nothing: its workspaces are the library's static device scratch array,
  * 32 MiB per device, which every call on that device shares and which keeps the last call's contents - calls that
  * overlap on one device race. Shapes whose partials would not fit it even as a single block (16 bytes per entry:
- * k * (dims + 2) above about 2.09 million) are refused with KM_EINVAL before anything is launched. The wide-row path (16 < dims <= 768 in
- * km_pass) needs a bf16 copy of the rows and is not used: those shapes run the rows path. ctx supplies the
+ * k * (dims + 2) above about 2.09 million) are refused with KM_EINVAL before anything is launched. The wide-row path (16 < dims <= 1536
+ * in km_pass) needs a bf16 copy of the rows and is not used: those shapes run the rows path. ctx supplies the
  * device, the scratch address and the error message; its own data and buffers are not touched. */
 int32_t km_pass_noalloc(km_ctx *ctx, const float *X, int64_t rows, int32_t dims, const float *C, int32_t k,
                         double *totals, uint32_t *labels, float *best, void *stream);
