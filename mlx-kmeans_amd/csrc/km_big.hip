@@ -688,12 +688,14 @@ __global__ __launch_bounds__(256) void k_big_label1(const uint16_t *__restrict__
 // key by an atomic minimum of (value bits << 32 | index): distances are non-negative or NaN, NaN is never taken
 // (strict '<'), so the key order is the value order and then the index order - the smallest distance, the lowest
 // index among equal ones, whatever order the ranges finish in. The key starts at (+inf, 0).
+// Without a list (over null) the kernel is the rows loop for all n_direct rows of a part, tile t holding rows
+// 64 t ..: the assignment of rows wider than the screen serves, whose rows fit no thread's registers.
 static constexpr int KB_FR = 64;        // rows per full-scan tile
 static constexpr int KB_FC = 64;        // centres per full-scan chunk
 static constexpr int KB_FSPLIT = 256;   // centres per range of the split full scan
 static constexpr uint64_t KB_FKEY0 = (uint64_t)0x7f800000u << 32;   // (+inf, label 0)
 __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ X, int d, const float *__restrict__ C,
-                                                      int k, const uint32_t *__restrict__ over,
+                                                      int k, const uint32_t *__restrict__ over, int64_t n_direct,
                                                       km_control *__restrict__ ctl, uint32_t *__restrict__ labels,
                                                       float *__restrict__ best, uint64_t *__restrict__ keys,
                                                       const int32_t *__restrict__ stop) {
@@ -703,8 +705,9 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
     __shared__ int64_t rows[KB_FR];
     const int tid = threadIdx.x;
     const int tr = tid >> 4, tc = tid & 15;   // rows 4 tr .. 4 tr + 3, centres 4 tc .. 4 tc + 3 of a chunk
-    const uint32_t total = ctl->n_over;
-    if (blockIdx.x == 0 && tid == 0) atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)total);
+    const uint32_t total = over ? ctl->n_over : (uint32_t)n_direct;
+    if (over && blockIdx.x == 0 && tid == 0)
+        atomicAdd((unsigned long long *)&ctl->fallback_rows, (unsigned long long)total);
     // work items: (tile, range) pairs, ranges of KB_FSPLIT centres when keys are given, else one range of all
     const int nsplit = keys ? (k + KB_FSPLIT - 1) / KB_FSPLIT : 1;
     const int csplit = keys ? KB_FSPLIT : k;
@@ -715,7 +718,10 @@ __global__ __launch_bounds__(256) void k_big_fullscan(const float *__restrict__ 
         const int cend = (cbeg + csplit < k) ? cbeg + csplit : k;
         const int nr = (int)((total - t0) < (uint32_t)KB_FR ? (total - t0) : (uint32_t)KB_FR);
         __syncthreads();   // the previous tile's rows are no longer read
-        if (tid < KB_FR) rows[tid] = tid < nr ? (int64_t)over[t0 + tid] : (int64_t)over[t0];
+        if (tid < KB_FR) {
+            const uint32_t q = t0 + (tid < nr ? tid : 0);
+            rows[tid] = over ? (int64_t)over[q] : (int64_t)q;
+        }
         __syncthreads();
         float bst[4];
         uint32_t bl[4];
@@ -1107,15 +1113,26 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (k <= KB_FSPLIT || !okeys) {
-        hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, ctl, labels, best,
-                           (uint64_t *)nullptr, stop);
+        hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, (int64_t)0, ctl, labels,
+                           best, (uint64_t *)nullptr, stop);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_big_fkeys_init, dim3(256), dim3(256), 0, s, okeys, ctl, stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, ctl, labels, best, okeys, stop);
+    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, (int64_t)0, ctl, labels, best,
+                       okeys, stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_big_fkeys_fin, dim3(256), dim3(256), 0, s, okeys, over, ctl, labels, best, stop);
+    return hipGetLastError();
+}
+
+hipError_t km_launch_rows_tiled(const float *X, int64_t n, int d, const float *C, int k, uint32_t *labels, float *best,
+                                const int32_t *stop, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (n > (int64_t)0xffffffffu - KB_FR) return hipErrorInvalidValue;
+    const int64_t tiles = (n + KB_FR - 1) / KB_FR;
+    hipLaunchKernelGGL(k_big_fullscan, dim3((unsigned)(tiles < 2048 ? tiles : 2048)), dim3(256), 0, s, X, d, C, k,
+                       (const uint32_t *)nullptr, n, (km_control *)nullptr, labels, best, (uint64_t *)nullptr, stop);
     return hipGetLastError();
 }
 

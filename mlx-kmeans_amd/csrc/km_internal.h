@@ -241,6 +241,10 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
                                 const int32_t *stop, hipStream_t s);
 // lite: the pass returns no per-row distances; single-candidate rows take their label without one. okeys: n words
 // for the full scan of the overflow rows split over centre ranges (above 256 centres; null: one range)
+// The rows loop for all n rows of a part, tiled (64 rows x 64 centres per block step, 32 dims at a time through
+// LDS): the same labels and best, bit for bit, for rows too wide for one thread's registers (n < 2^32 - 64).
+hipError_t km_launch_rows_tiled(const float *X, int64_t n, int d, const float *C, int k, uint32_t *labels, float *best,
+                                const int32_t *stop, hipStream_t s);
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
                                  uint32_t *labels, float *best, int lite, uint64_t *okeys, const int32_t *stop,

@@ -5,7 +5,9 @@ From 49 K-steps of 16 dims the screen runs one block per CU (its 32 rows per wav
 up to 384 registers) and the per-cluster sums take 14 to 24 dims per lane. Labels and best must be the rows loop's
 (core.py:263-274) bit for bit against the oracle on every row, on every path that serves the shape; the totals
 within the reference's accuracy bar (tests/accuracy.py:91-99); one Lloyd step against the oracle's; and a fit loop
-whose passes take the change-only sums must reach the centres that single steps with full sums reach.
+whose passes take the change-only sums must reach the centres that single steps with full sums reach. Rows wider
+than 1536 dims take the rows loop, in its tiled form from four centres on (as does the forced rows path from 65
+dims), held to the same bar.
 """
 import numpy as np
 import pytest
@@ -101,4 +103,34 @@ def test_wide_rows_fit_loop_matches_single_steps(lib, d, k, parts):
     assert abs(in_fit - inertia) <= 1e-6 * inertia
     C2, in2, _, _ = ctx.fit(C0, steps, -1.0)
     assert np.array_equal(C2, C_fit) and in2 == in_fit
+    ctx.close()
+
+
+@pytest.mark.parametrize("n,d,k,parts", [(3_000, 2048, 100, 1), (2_001, 3000, 300, 2), (1_500, 4096, 1000, 1),
+                                         (1_000, 1537, 4, 1), (700, 2500, 3, 1), (5_000, 100, 64, 2)])
+def test_rows_wider_than_the_screen_match_the_oracle(lib, n, d, k, parts):
+    import oracle
+    X, C, slices = _blobs(n * 7 + d + k, n, d, k, max(k // 4, 3), parts)
+    ol, ob = oracle.assign(X, C)
+    ot = oracle.totals(X, ol, ob, k)
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(slices)
+    for path in ("auto", "rows"):
+        say(f"[gpu] rows loop n={n} d={d} k={k} parts={parts} path={path}")
+        tot, labels, best = ctx.run_pass(C, path=lib.PATHS[path], labels=True, best=True)
+        if d > 1536:
+            assert ctx.last_path() == "rows"
+        assert np.array_equal(labels, ol), (path, np.flatnonzero(labels != ol)[:10])
+        assert np.array_equal(best.view(np.uint32), ob.view(np.uint32)), path
+        counts = np.rint(tot[:, 0]).astype(np.int64)
+        assert np.array_equal(counts, np.rint(ot[:, 0]).astype(np.int64)), path
+        used = counts > 0
+        err = float(np.max(np.abs(tot[used, 2:] - ot[used, 2:]) / counts[used, None])) / scale
+        assert err <= CENTRE_TOL, (path, err)
+    C1, inertia, n_empty = ctx.lloyd_step(C)
+    R1, r_in, r_empty, _, _, _ = oracle.lloyd_step(X, C)
+    assert n_empty == r_empty
+    assert abs(inertia - r_in) <= 1e-6 * r_in
+    assert float(np.max(np.abs(C1.astype(np.float64) - R1))) / scale <= CENTRE_TOL
     ctx.close()
