@@ -33,6 +33,7 @@ DESCRIPTIONS = {
     "lowd_d8": "10M x 8 fp32, k=8, 8-component diagonal mixture",
     "pixels_d4": "96M x 4 fp32, k=12, 12-class clipped correlated mixture",
     "embed_d768": "1M x 768 fp32, k=1024, unit-norm vMF-style embeddings",
+    "embed_d1536": "1M x 1536 fp32, k=1024, unit-norm vMF-style embeddings",
 }
 
 
@@ -218,7 +219,7 @@ def main():
     kname, (kms, kcount) = max(prof.items(), key=lambda kv: kv[1][0])
     avg_ms = kms / kcount
     log("[bench] kernels: " + ", ".join(f"{k_}: {v[0] / v[1] * 1e3:.1f} us x{v[1]}" for k_, v in prof.items()))
-    if a.workload == "embed_d768":
+    if a.workload.startswith("embed_d"):
         flops = 2.0 * n * k * d
         achieved = flops / (avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -11,6 +11,7 @@
                    rows; 30 iterations
     embed_d768     1M x 768, k=1024: unit rows normalize(centre + N(0, 0.15^2 I)) around 1024 random unit
                    centres; start: 1024 seeded rows; 15 iterations
+    embed_d1536    the same at 1536 dims (the widest rows the matrix-core screen takes)
 
 Every generator takes n (rows) so tests can draw the same distribution at smaller sizes.
 """
@@ -125,9 +126,8 @@ def pixels_d4(n=96_000_000, seed=0):
     return dict(name="pixels_d4", X=X, C0=C0, k=k, iters=30)
 
 
-def embed_d768(n=1_000_000, seed=0, k=1024):
+def _unit_rows(name, n, d, seed, k):
     rng = np.random.default_rng(seed)
-    d = 768
     cen = rng.standard_normal((k, d), dtype=np.float32)
     cen /= np.linalg.norm(cen, axis=1, keepdims=True)
     X = np.empty((n, d), np.float32)
@@ -138,7 +138,15 @@ def embed_d768(n=1_000_000, seed=0, k=1024):
         r = cen[lab] + np.float32(0.15) * rng.standard_normal((b - a, d), dtype=np.float32)
         X[a:b] = r / np.linalg.norm(r, axis=1, keepdims=True)
     C0 = _distinct_rows(rng, X, k)
-    return dict(name="embed_d768", X=X, C0=C0, k=k, iters=15)
+    return dict(name=name, X=X, C0=C0, k=k, iters=15)
+
+
+def embed_d768(n=1_000_000, seed=0, k=1024):
+    return _unit_rows("embed_d768", n, 768, seed, k)
+
+
+def embed_d1536(n=1_000_000, seed=0, k=1024):
+    return _unit_rows("embed_d1536", n, 1536, seed, k)
 
 
 WORKLOADS = {
@@ -147,4 +155,5 @@ WORKLOADS = {
     "outliers_d32": outliers_d32,
     "pixels_d4": pixels_d4,
     "embed_d768": embed_d768,
+    "embed_d1536": embed_d1536,
 }
