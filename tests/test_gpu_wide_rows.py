@@ -134,3 +134,23 @@ def test_rows_wider_than_the_screen_match_the_oracle(lib, n, d, k, parts):
     assert abs(inertia - r_in) <= 1e-6 * r_in
     assert float(np.max(np.abs(C1.astype(np.float64) - R1))) / scale <= CENTRE_TOL
     ctx.close()
+
+
+@pytest.mark.parametrize("d,k", [(3072, 32), (1536, 48)])
+def test_estimator_on_wide_rows(lib, d, k):
+    """KMeans end to end (k-means++ seeding on the device, the GPU-resident loop, final scoring, predict) at 3072
+    dims (the tiled rows loop) and 1536 dims (the screen at 96 K-steps): labels_ are the oracle's assignment to the
+    returned centres bit for bit, inertia_ the oracle's, predict(X) returns labels_."""
+    import oracle
+    from mlx_kmeans import KMeans
+    rng = np.random.default_rng(d + k)
+    n = 6_000
+    cen = rng.standard_normal((k, d)).astype(np.float32)
+    X = (cen[rng.integers(0, k, n)] + 0.5 * rng.standard_normal((n, d))).astype(np.float32)
+    say(f"[gpu] KMeans on {n} x {d}, k = {k}")
+    km = KMeans(n_clusters=k, max_iter=8, random_state=3).fit(X)
+    ol, ob = oracle.assign(X, km.cluster_centers_)
+    assert np.array_equal(km.labels_, ol.astype(np.int64))
+    ref = float(ob.astype(np.float64).sum())
+    assert abs(km.inertia_ - ref) <= 1e-5 * ref
+    assert np.array_equal(km.predict(X), km.labels_)
