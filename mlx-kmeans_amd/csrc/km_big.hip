@@ -11,7 +11,8 @@
 //                   inside the error window around it - every centre that can hold the exact minimum
 //   k_big_rescore   the rows loop (core.py:263-274) on those candidates only, ascending index, strict '<'
 //   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every
-//                   centre, 64 rows x 64 centres per block step
+//                   centre, 64 rows x 64 centres per block step; without a row list, every row of a part (the
+//                   rows loop's tiled form, km_launch_rows_tiled)
 //   k_big_hist/scan/scatter   a stable counting sort of the rows by label; then the per-cluster float64 sums in
 //                   row order, in fixed chunks of sorted rows (km_chunks.hip): the totals of the pass
 //
