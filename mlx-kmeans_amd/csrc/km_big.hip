@@ -40,6 +40,9 @@ static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
 static constexpr int KB_SLICE = 25;       // most A-operand K-steps per LDS slice (1 KB each): 768 dims take two
                                           // slices per chunk, so two block barriers and a prefetch of half a chunk
 static constexpr int KB_WAVES = 4;        // waves per screen block (32 rows each)
+// A-fragment K-steps in flight above 48 K-steps, where one wave per SIMD has no other wave to cover the LDS
+// latency (500k x 960 / 1536, k = 1024, us per screen: 3 steps 1795 / 2318, 6 steps 1720 / 2262, 9 steps 1726 / 2232)
+static constexpr int KB_PF_WIDE = 9;
 static constexpr int KB_OVER = 0xffff;    // ncand value: scan every centre
 static constexpr double KB_APPROX_LIMIT = 65504.0 / 4;   // the reference's APPROX_FP16_LIMIT (core.py:1035)
 
@@ -327,28 +330,29 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (g + 1 < G) issue(g + 1);
-            // A fragments three K-steps ahead of their MFMA (four registers sets in rotation), the reads and MFMAs
-            // interleaved one for one: the LDS latency is covered by three MFMAs instead of two
-            bf16x8 Ab[4];
+            // A fragments PF K-steps ahead of their MFMA (PF + 1 register sets in rotation), the reads and MFMAs
+            // interleaved one for one: the LDS latency is covered by PF MFMAs
+            constexpr int PF = DS > 48 ? KB_PF_WIDE : 3;
+            bf16x8 Ab[PF + 1];
 #pragma unroll
-            for (int j = 0; j < 3; j++)
+            for (int j = 0; j < PF; j++)
                 if (sl * SLK + j < AK && j < SLK) Ab[j] = *reinterpret_cast<const bf16x8 *>(cur + j * 1024 + lane * 16);
 #pragma unroll
             for (int j = 0; j < SLK; j++) {
                 const int s = sl * SLK + j;   // compile-time after unrolling
-                if (j + 3 < SLK && s + 3 < AK)
-                    Ab[(j + 3) & 3] = *reinterpret_cast<const bf16x8 *>(cur + (j + 3) * 1024 + lane * 16);
+                if (j + PF < SLK && s + PF < AK)
+                    Ab[(j + PF) % (PF + 1)] = *reinterpret_cast<const bf16x8 *>(cur + (j + PF) * 1024 + lane * 16);
                 if (s < AK)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Ab[j & 3], s < DS ? B[s < DS ? s : 0] : Bone, acc, 0,
-                                                                   0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Ab[j % (PF + 1)], s < DS ? B[s < DS ? s : 0] : Bone,
+                                                                   acc, 0, 0, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);   // three LDS reads,
+            __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);   // PF LDS reads,
 #pragma unroll
-            for (int j = 0; j < SLK - 3; j++) {                    // then MFMA, LDS read, ...,
+            for (int j = 0; j < SLK - PF; j++) {                    // then MFMA, LDS read, ...,
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // and the last three MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);   // and the last PF MFMAs
         }
     };
 
