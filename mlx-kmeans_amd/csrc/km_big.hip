@@ -39,6 +39,10 @@ static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
 static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
 static constexpr int KB_SLICE = 25;       // most A-operand K-steps per LDS slice (1 KB each): 768 dims take two
                                           // slices per chunk, so two block barriers and a prefetch of half a chunk
+// Above 48 K-steps one block per CU has the LDS to itself: slices of up to 49 K-steps, two per chunk (500k x 960 /
+// 1536, k = 1024, us per screen: 25-step slices 1721 / 2224, 49-step slices 1636 / 2205)
+static constexpr int KB_SLICE_WIDE = 49;
+__host__ __device__ constexpr int kb_slice(int ds) { return ds > 48 ? KB_SLICE_WIDE : KB_SLICE; }
 static constexpr int KB_WAVES = 4;        // waves per screen block (32 rows each)
 // A-fragment K-steps in flight above 48 K-steps, where one wave per SIMD has no other wave to cover the LDS
 // latency (500k x 960 / 1536, k = 1024, us per screen: 3 steps 1795 / 2318, 6 steps 1720 / 2262, 9 steps 1726 / 2232)
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
     // finite) and the largest |c|^2 of the centres. Otherwise the pass is exact.
     if (approx) approx = sqrt((double)kb_f32(*xmax) * (double)maxes[1]) < KB_APPROX_LIMIT;
     extern __shared__ float lds[];
-    char *ring = reinterpret_cast<char *>(lds);   // two slices of at most KB_SLICE K-steps, 1 KB each
+    char *ring = reinterpret_cast<char *>(lds);   // two slices of at most kb_slice(DS) K-steps, 1 KB each
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int h = lane >> 5;
     const int64_t ntiles = (n + 31) / 32;
@@ -300,7 +304,7 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
 
     // A operand slices: chunk ch is SPC slices of SLK K-steps (the last possibly shorter), staged through a
     // two-slice LDS ring; slice g is loaded while slice g - 1 is multiplied.
-    constexpr int SPC = (AK + KB_SLICE - 1) / KB_SLICE;
+    constexpr int SPC = (AK + kb_slice(DS) - 1) / kb_slice(DS);
     constexpr int SLK = (AK + SPC - 1) / SPC;
     const int GP = nchunks * SPC;
     const int G = GP;
@@ -1083,7 +1087,7 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
     // exact=False approximates from 64 dims, and only under the half-precision guard (checked in the kernel);
     // below 64 dims the reference's dispatch runs its exact kernels (core.py:2036-2042)
     const int approx = (mode == KM_APPROX && d >= KM_APPROX_MIN_DIMS) ? 1 : 0;
-    const int ak = pl.DS + 1, spc = (ak + KB_SLICE - 1) / KB_SLICE, slk = (ak + spc - 1) / spc;
+    const int ak = pl.DS + 1, spc = (ak + kb_slice(pl.DS) - 1) / kb_slice(pl.DS), slk = (ak + spc - 1) / spc;
     const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * KB_HALF * 64 * (pack ? 4 : 6);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
