@@ -154,3 +154,28 @@ def test_estimator_on_wide_rows(lib, d, k):
     ref = float(ob.astype(np.float64).sum())
     assert abs(km.inertia_ - ref) <= 1e-5 * ref
     assert np.array_equal(km.predict(X), km.labels_)
+
+
+@pytest.mark.parametrize("d,k", [(2048, 40), (1000, 70), (200, 16)])
+def test_non_finite_rows_on_wide_paths(lib, d, k):
+    """Rows holding NaN or +-inf, and one centre with an infinite coordinate: labels and best are still the rows
+    loop's bit for bit (a NaN distance never compares below, a row whose distances are all NaN or +inf keeps label 0
+    and best +inf) on the tiled rows loop and the wide-row screen."""
+    import oracle
+    X, C, _ = _blobs(d * 3 + k, 3_000, d, k, 8)
+    X[5, 3] = np.nan
+    X[17, :] = np.nan
+    X[40, 0] = np.inf
+    X[41, 1] = -np.inf
+    C[k - 1, 2] = np.inf
+    ol, ob = oracle.assign(X, C)
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    for path in ("auto", "mfma", "rows"):
+        if path == "mfma" and d > 1536:
+            continue
+        say(f"[gpu] non-finite rows d={d} k={k} path={path}")
+        _, labels, best = ctx.run_pass(C, path=lib.PATHS[path], labels=True, best=True)
+        assert np.array_equal(labels, ol), (path, np.flatnonzero(labels != ol)[:10])
+        assert np.array_equal(best.view(np.uint32), ob.view(np.uint32)), path
+    ctx.close()
