@@ -179,3 +179,27 @@ def test_non_finite_rows_on_wide_paths(lib, d, k):
         assert np.array_equal(labels, ol), (path, np.flatnonzero(labels != ol)[:10])
         assert np.array_equal(best.view(np.uint32), ob.view(np.uint32)), path
     ctx.close()
+
+
+def test_approx_on_the_widest_screen(lib):
+    """exact=False at 1536 dims (unit rows, so the half-precision guard holds): best is the oracle's distance to the
+    chosen label bit for bit and never below the exact best, the inertia is at least the exact one, labels disagree
+    with exact mode on at most 10 % of rows, and the counts match the labels."""
+    import oracle
+    from mlx_kmeans import synthetic
+    w = synthetic.embed_d1536(n=100_000, k=256)
+    X, C0, k = w["X"], w["C0"], w["k"]
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say("[gpu] exact=False at 1536 dims")
+    te, le, be = ctx.run_pass(C0, mode=lib.KM_EXACT, labels=True, best=True)
+    ta, la, ba = ctx.run_pass(C0, mode=lib.KM_APPROX, labels=True, best=True)
+    assert ctx.last_path() == "mfma"
+    assert np.array_equal(ba.view(np.uint32), oracle.distances_to(X, C0, la).view(np.uint32))
+    assert np.all(ba >= be)
+    assert float(ta[:, 1].sum()) >= float(te[:, 1].sum())
+    dis = float(np.mean(la != le))
+    say(f"[gpu]   approx label disagreement {dis:.4%}")
+    assert dis <= 0.10
+    assert np.array_equal(np.rint(ta[:, 0]).astype(np.int64), np.bincount(la, minlength=k))
+    ctx.close()
