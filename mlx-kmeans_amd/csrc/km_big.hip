@@ -1013,6 +1013,7 @@ static screen_fn kb_screen_for(int DS) {
         case 24: return k_big_screen<24, PACK>;
         case 32: return k_big_screen<32, PACK>;
         case 48: return k_big_screen<48, PACK>;
+        case 60: return k_big_screen<60, PACK>;
         case 64: return k_big_screen<64, PACK>;
         case 96: return k_big_screen<96, PACK>;
         default: return nullptr;
@@ -1021,7 +1022,7 @@ static screen_fn kb_screen_for(int DS) {
 
 static int kb_ds(int d) {
     const int s = (d + 15) / 16;
-    const int opts[] = {2, 4, 8, 16, 24, 32, 48, 64, 96};
+    const int opts[] = {2, 4, 8, 16, 24, 32, 48, 60, 64, 96};   // 60: 960-dim rows without padding to 1024
     for (int o : opts)
         if (s <= o) return o;
     return 0;
