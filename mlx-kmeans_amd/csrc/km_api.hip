@@ -22,6 +22,10 @@
 
 #define KM_ABI_VERSION 1
 static const int KM_FIT_BATCH = 8;
+// In the fit loop a pass that accumulates only changed rows adds its (float32 fused, float64 wide-row) change sums
+// to the previous totals; every KM_REANCHOR_PASSES passes after a recording pass, one pass records every row again,
+// so the totals never carry more than that many passes of change rounding.
+static const int KM_REANCHOR_PASSES = 32;
 
 template <class T>
 struct DBuf {
@@ -781,9 +785,6 @@ extern "C" int32_t km_pass(km_ctx *c, const float *C, int32_t k, int32_t mode, i
 // the device (km_reloc.hip): the host reads back only the number of empty clusters.
 static int relocate(km_ctx *c, int k, int mode, int path, int pass, int *n_empty_out) {
     const int d = c->d;
-    if (c->n > (int64_t)UINT32_MAX)
-        return fail(c, KM_EINVAL, "relocating empty clusters counts rows in 32 bits: %lld rows is too many",
-                    (long long)c->n);
     int r = run_labels(c, k, mode, path, pass);
     if (r) return r;
     const int64_t nb = km_reloc_blocks(c->n, c->dev.cus);
@@ -928,7 +929,7 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     bool use_ls = false;
     if ((r = prepare_label_state(c, k, &use_ls))) return r;
     // the pass that records every label (the first, and the first after a relocation); later passes accumulate
-    // only the rows whose label changed
+    // only the rows whose label changed, and every KM_REANCHOR_PASSES-th pass after it records again
     int rec_pass = 0;
     int pass = 0, relocated = 0;
     // with timing on, an event at every pass boundary on the stream: the per-pass times km_profile_passes reads
@@ -942,7 +943,9 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
     while (pass < max_iter) {
         const int batch = std::min(KM_FIT_BATCH, max_iter - pass);
         for (int i = 0; i < batch; i++) {
-            const int lm = !use_ls ? KM_LSTATE_NONE : (pass + i == rec_pass ? KM_LSTATE_RECORD : KM_LSTATE_DELTA);
+            const int since = pass + i - rec_pass;
+            const int lm = !use_ls ? KM_LSTATE_NONE
+                                   : (since % KM_REANCHOR_PASSES == 0 ? KM_LSTATE_RECORD : KM_LSTATE_DELTA);
             mark(i == 0);
             if ((r = queue_iteration(c, k, mode, path, pass + i, tol, spherical, lm))) return r;
         }

@@ -21,8 +21,13 @@ namespace {
 constexpr int RL_BINS = 2048;
 constexpr int RL_TB = 256;
 // state words: 0 m (rows to take), 1 key prefix, 2 rows still to take at the prefix, 3 largest key,
-// 4 rows with a key above T collected, 5 empty clusters; histogram from word 16
+// 4 rows with a key above T collected, 5 empty clusters; from word 16 the histogram, RL_BINS 64-bit counts (a bin
+// can hold more than 2^32 rows)
 enum { RL_M = 0, RL_PREFIX, RL_NEED, RL_KMAX, RL_NGT, RL_NEMPTY, RL_HIST = 16 };
+
+__device__ __forceinline__ unsigned long long *rl_hist(uint32_t *st) {
+    return reinterpret_cast<unsigned long long *>(st + RL_HIST);
+}
 
 __device__ __forceinline__ uint32_t rl_key(float b) { return b > 0.0f ? __float_as_uint(b) : 0u; }
 
@@ -47,7 +52,7 @@ __global__ __launch_bounds__(1024) void k_rl_init(const double *__restrict__ tot
                                                   uint32_t *__restrict__ st, int32_t *__restrict__ empties) {
     __shared__ uint32_t s_w[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < RL_HIST + RL_BINS; e += 1024) st[e] = 0;
+    for (int e = tid; e < RL_HIST + 2 * RL_BINS; e += 1024) st[e] = 0;
     uint32_t base = 0;
     for (int c0 = 0; c0 < k; c0 += 1024) {
         const int c = c0 + tid;
@@ -91,7 +96,7 @@ __global__ __launch_bounds__(RL_TB) void k_rl_hist(const float *__restrict__ bes
     }
     __syncthreads();
     for (int e = threadIdx.x; e < RL_BINS; e += RL_TB)
-        if (h[e]) atomicAdd(&st[RL_HIST + e], h[e]);
+        if (h[e]) atomicAdd(rl_hist(st) + e, (unsigned long long)h[e]);
     if (shift == 21) {
         for (int off = 32; off > 0; off >>= 1) {
             const uint32_t o = __shfl_xor(kmax, off);
@@ -105,18 +110,19 @@ __global__ __launch_bounds__(RL_TB) void k_rl_hist(const float *__restrict__ bes
 __global__ __launch_bounds__(64) void k_rl_pick(uint32_t *st, int shift) {
     if (st[RL_M] == 0) return;
     if (threadIdx.x == 0) {
-        uint32_t need = st[RL_NEED], cum = 0;
+        const uint32_t need = st[RL_NEED];
+        unsigned long long cum = 0;   // below need (at most m) until the loop stops
         int b = RL_BINS - 1;
         for (; b > 0; b--) {
-            const uint32_t h = st[RL_HIST + b];
+            const unsigned long long h = rl_hist(st)[b];
             if (cum + h >= need) break;
             cum += h;
         }
         st[RL_PREFIX] |= (uint32_t)b << shift;
-        st[RL_NEED] = need - cum;
+        st[RL_NEED] = need - (uint32_t)cum;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < RL_BINS; e += 64) st[RL_HIST + e] = 0;
+    for (int e = threadIdx.x; e < RL_BINS; e += 64) rl_hist(st)[e] = 0;
 }
 
 // Rows with key T in each block's contiguous range.
@@ -138,14 +144,15 @@ __global__ __launch_bounds__(RL_TB) void k_rl_count(const float *__restrict__ be
     }
 }
 
-// Exclusive scan of the per-block tie counts, in block (row) order.
+// Exclusive scan of the per-block tie counts, in block (row) order. An offset is only compared with the rows still
+// to take (at most m < 2^32), so offsets saturate at 2^32 - 1 instead of wrapping.
 __global__ __launch_bounds__(64) void k_rl_scan(uint32_t *tiecnt, int nb, const uint32_t *st) {
     if (st[RL_M] == 0) return;
     if (threadIdx.x == 0) {
-        uint32_t run = 0;
+        unsigned long long run = 0;
         for (int b = 0; b < nb; b++) {
             const uint32_t v = tiecnt[b];
-            tiecnt[b] = run;
+            tiecnt[b] = run < 0xffffffffull ? (uint32_t)run : 0xffffffffu;
             run += v;
         }
     }
@@ -159,7 +166,7 @@ __global__ __launch_bounds__(RL_TB) void k_rl_collect(const float *__restrict__ 
     if (m == 0) return;
     const uint32_t T = st[RL_PREFIX], need = st[RL_NEED];
     const int64_t r0 = (int64_t)blockIdx.x * rpb, r1 = r0 + rpb < n ? r0 + rpb : n;
-    uint32_t run = tieoff[blockIdx.x];
+    unsigned long long run = tieoff[blockIdx.x];
     for (int64_t c0 = r0; c0 < r1; c0 += RL_TB) {   // block-uniform trip count: every thread reaches the barriers
         const int64_t r = c0 + threadIdx.x;
         const uint32_t key = r < r1 ? rl_key(best[r]) : 0u;
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(1024) void k_rl_apply(const uint32_t *__restrict__ 
 
 }  // namespace
 
-size_t km_reloc_state_words() { return RL_HIST + RL_BINS; }
+size_t km_reloc_state_words() { return RL_HIST + 2 * RL_BINS; }
 int64_t km_reloc_blocks(int64_t n, int cus) {
     int64_t nb = (n + 4095) / 4096;
     const int64_t cap = (int64_t)cus * 16;

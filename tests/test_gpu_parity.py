@@ -446,6 +446,37 @@ def test_embed_workload_full_size(lib):
     ctx.close()
 
 
+@pytest.mark.parametrize("n,d,k,path", [(200_003, 32, 64, "mfma"), (100_003, 128, 64, "wide")])
+def test_fit_loop_totals_after_300_passes(lib, n, d, k, path):
+    """KMeans' default max_iter is 300. On uniform data rows keep changing cluster for hundreds of passes (about
+    150 of 200k per pass at pass 300), so the fit loop's change-only passes keep adding to the carried totals.
+    The first 299 passes of a 300-pass fit are a 299-pass fit (reruns are bit-identical), so one full
+    km_lloyd_step from the 299-pass fit's centres scores the same labels as the 300-pass fit's last pass: its
+    centres must agree within 1e-6 of the RMS and its inertia within 1e-6 (the reference recomputes its sums
+    every pass, core.py:2209-2242)."""
+    rng = np.random.default_rng(300 + d)
+    X = rng.random((n, d), dtype=np.float32)
+    C0 = X[rng.choice(n, k, replace=False)].copy()
+    scale = float(np.sqrt((X.astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] 300-pass fit n={n} d={d} k={k}")
+    C300, in300, it300, _ = ctx.fit(C0, 300, -1.0)
+    assert it300 == 300
+    assert ctx.last_path() == "mfma"
+    C299, _, it299, _ = ctx.fit(C0, 299, -1.0)
+    assert it299 == 299
+    _, lab_a, _ = ctx.run_pass(C299, labels=True)
+    _, lab_b, _ = ctx.run_pass(ctx.lloyd_step(C299)[0], labels=True)
+    say(f"[gpu]   rows changing cluster at pass 300: {int((lab_a != lab_b).sum())}")
+    C_ref, in_ref, _ = ctx.lloyd_step(C299)
+    err = float(np.max(np.abs(C300.astype(np.float64) - C_ref.astype(np.float64)))) / scale
+    say(f"[gpu]   centre error {err:.2e}, inertia {in300:.9e} vs {in_ref:.9e}")
+    assert err <= 1e-6
+    assert abs(in300 - in_ref) <= 1e-6 * in_ref
+    ctx.close()
+
+
 @pytest.mark.parametrize("d,k,parts,path", [(32, 64, 1, "mfma"), (16, 40, 2, "mfma"), (64, 32, 1, "mfma"),
                                             (32, 20, 3, "mfma"), (16, 64, 1, "mfma"), (4, 12, 1, "fused"),
                                             (8, 8, 2, "fused"), (2, 40, 1, "fused"), (3, 30, 3, "fused"),

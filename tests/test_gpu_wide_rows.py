@@ -39,7 +39,7 @@ def _blobs(seed, n, d, k, true_k, parts=1):
 
 @pytest.mark.parametrize("n,d,k,parts", [(20_000, 960, 304, 1), (10_007, 1000, 100, 2), (8_000, 1536, 64, 1),
                                          (6_001, 1100, 257, 3), (30_000, 1024, 1024, 1), (5_000, 770, 33, 1),
-                                         (6_000, 1040, 4500, 1)])
+                                         (6_000, 1040, 4500, 1), (9_001, 769, 200, 1), (7_003, 784, 65, 2)])
 def test_wide_rows_match_the_oracle(lib, n, d, k, parts):
     import oracle
     X, C, slices = _blobs(n + d + k, n, d, k, max(k // 4, 3), parts)

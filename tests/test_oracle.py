@@ -256,3 +256,44 @@ def test_normalise_pinned(oracle):
     want = np.where(nrm > 0, C64 / np.where(nrm > 0, nrm, 1), 0.0)
     assert np.all(np.abs(N.astype(np.float64) - want) <= 4 * 2.0**-24 * np.maximum(np.abs(want), 2.0**-30))
     assert np.all(N[7] == 0.0) and np.array_equal(N[8], C[8])
+
+
+def test_fit_from_stop_rule_hand_computed(oracle):
+    """KMeans._one_run's loop (estimator.py:137-150) on five 1-D points worked by hand. From C0 = [0, 1] the steps
+    report the inertia of their input centres: 302 ([0, 1] -> [0, 8.5]), 21.75 (-> [0.5, 11]), 2.5 (-> [0.5, 11]),
+    2.5. The loop stops after the first step whose inertia is within tol * prev of the previous one, never after the
+    first step (no previous inertia), and the returned inertia scores the returned centres (estimator.py:201-204)."""
+    X = np.array([[0.], [1.], [10.], [11.], [12.]], np.float32)
+    C0 = np.array([[0.], [1.]], np.float32)
+    cases = [  # (max_iter, tol) -> (n_iter, centres, final inertia)
+        ((50, 0.0), (4, [0.5, 11.0], 2.5)),       # 2.5 == 2.5 at step 4
+        ((50, 0.9), (3, [0.5, 11.0], 2.5)),       # |21.75 - 2.5| = 19.25 <= 0.9 * 21.75 = 19.575
+        ((50, 0.885), (4, [0.5, 11.0], 2.5)),     # 19.25 > 0.885 * 21.75 = 19.249: one more step
+        ((50, 1e9), (2, [0.5, 11.0], 2.5)),       # step 1 has no previous inertia; step 2 stops
+        ((1, 0.0), (1, [0.0, 8.5], 21.75)),       # max_iter: the centres of step 1, scored
+        ((2, 0.0), (2, [0.5, 11.0], 2.5)),
+    ]
+    for (max_iter, tol), (n_iter, C_want, inertia_want) in cases:
+        C, inertia, it, labels = oracle.fit_from(X, C0, max_iter=max_iter, tol=tol)
+        assert it == n_iter, (max_iter, tol, it)
+        assert C[:, 0].tolist() == C_want, (max_iter, tol, C)
+        assert inertia == inertia_want, (max_iter, tol, inertia)
+        assert labels.tolist() == [0, 0, 1, 1, 1]   # both [0, 8.5] and [0.5, 11] send 1 to centre 0
+
+
+def test_fit_from_spherical_order_hand_computed(oracle):
+    """spherical=True (estimator.py:134-135, 143-144): the starting centres are normalised, and every step's
+    centres are normalised before the stop test. On X = [(1,0), (0,1), (1,1)] from C0 = [(2,0), (0,3)]: step 1
+    with [(1,0), (0,1)] sends (1,1) to centre 0 on a tie (inertia 1), the new centre 0 is (1, 0.5) / |.|
+    = (2, 1) / sqrt(5); step 2 reports 5 - 2 sqrt(5) and step 3 the same, so the loop stops after three steps.
+    Without the per-step normalisation step 2 would report 0.5 and centre 0 would stay (1, 0.5)."""
+    X = np.array([[1., 0.], [0., 1.], [1., 1.]], np.float32)
+    C0 = np.array([[2., 0.], [0., 3.]], np.float32)
+    C, inertia, it, labels = oracle.fit_from(X, C0, max_iter=50, tol=0.0, spherical=True)
+    assert it == 3
+    assert labels.tolist() == [0, 1, 0]
+    c0 = np.array([2.0, 1.0]) / np.sqrt(5.0)
+    assert np.allclose(C.astype(np.float64), [c0, [0.0, 1.0]], rtol=0, atol=2e-7)
+    assert abs(inertia - (5 - 2 * np.sqrt(5.0))) <= 1e-6
+    C, inertia, it, _ = oracle.fit_from(X, C0, max_iter=1, tol=0.0, spherical=True)
+    assert it == 1 and np.allclose(C.astype(np.float64), [c0, [0.0, 1.0]], rtol=0, atol=2e-7)

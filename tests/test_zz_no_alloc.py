@@ -2,7 +2,8 @@
 
 Two calls in a row on one context, the second with fewer rows (the scratch array keeps the first call's
 contents); each must give km_pass's labels and best bit for bit, its counts exactly, and its sums and inertia
-within 1e-6 relative (the same kernel family, summed over as many or fewer row blocks). Also: a shape whose
+within 1e-6 relative (the same kernel family, summed over as many or fewer row blocks). Also two calls queued on
+one stream with no synchronisation between them. Also: a shape whose
 partials cannot fit the scratch is refused with a clear error before any launch.
 """
 import ctypes
@@ -54,26 +55,54 @@ class _Hip:
         return out
 
 
-def _noalloc(lib, ctx, X, C):
-    """One km_pass_noalloc call on a stream of the test's own -> (totals f64, labels u32, best f32)."""
+def _noalloc_calls(lib, ctx, cases):
+    """km_pass_noalloc once per (X, C) in `cases`, all queued on one stream of the test's own with no
+    synchronisation between the calls -> [(totals f64, labels u32, best f32)] per call."""
     hip = _Hip(lib.lib())
-    n, d = X.shape
-    k = C.shape[0]
-    tot0 = np.full((k, d + 2), np.nan)
-    lab0 = np.full(n, 0xffffffff, np.uint32)
-    bst0 = np.full(n, np.nan, np.float32)
-    bufs = [hip.put(X), hip.put(np.ascontiguousarray(C, np.float32)), hip.put(tot0), hip.put(lab0), hip.put(bst0)]
     stream = ctypes.c_void_p()
     hip.check(hip.L.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    calls, bufs = [], []
     try:
-        rc = lib.lib().km_pass_noalloc(ctx._h, bufs[0], n, d, bufs[1], k, bufs[2], bufs[3], bufs[4], stream)
+        for X, C in cases:
+            n, d = X.shape
+            k = C.shape[0]
+            like = (np.full((k, d + 2), np.nan), np.full(n, 0xffffffff, np.uint32), np.full(n, np.nan, np.float32))
+            b = [hip.put(X), hip.put(np.ascontiguousarray(C, np.float32))] + [hip.put(a) for a in like]
+            bufs += b
+            rc = lib.lib().km_pass_noalloc(ctx._h, b[0], n, d, b[1], k, b[2], b[3], b[4], stream)
+            ctx._check(rc)
+            calls.append((b, like))
         hip.check(hip.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
-        ctx._check(rc)
-        return hip.get(bufs[2], tot0), hip.get(bufs[3], lab0), hip.get(bufs[4], bst0)
+        return [tuple(hip.get(p, a) for p, a in zip(b[2:], like)) for b, like in calls]
     finally:
+        hip.check(hip.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
         hip.L.hipStreamDestroy(stream)
-        for b in bufs:
-            hip.L.hipFree(b)
+        for p in bufs:
+            hip.L.hipFree(p)
+
+
+def _noalloc(lib, ctx, X, C):
+    """One km_pass_noalloc call on a stream of the test's own -> (totals f64, labels u32, best f32)."""
+    return _noalloc_calls(lib, ctx, [(X, C)])[0]
+
+
+def _km_pass(lib, X, C):
+    ref = lib.Context()
+    ref.set_parts([X])
+    out = ref.run_pass(C, labels=True, best=True)
+    ref.close()
+    return out
+
+
+def _same(got, want):
+    (t1, l1, b1), (t0, l0, b0) = got, want
+    assert np.array_equal(l1, l0), np.flatnonzero(l1 != l0)[:10]
+    assert np.array_equal(b1.view(np.uint32), b0.view(np.uint32))
+    assert np.array_equal(np.rint(t1[:, 0]), np.rint(t0[:, 0]))
+    fin = np.isfinite(t0)
+    assert np.array_equal(fin, np.isfinite(t1))
+    scale = np.maximum(np.abs(t0[fin]), 1.0)
+    assert np.all(np.abs(t1[fin] - t0[fin]) <= 1e-6 * scale)
 
 
 def _data(seed, n, d, k):
@@ -85,24 +114,31 @@ def _data(seed, n, d, k):
     return X, C
 
 
-@pytest.mark.parametrize("d,k", [(32, 64), (4, 12), (16, 40), (48, 100), (3, 300)])
-def test_noalloc_pass_matches_km_pass(lib, d, k):
+# (dims, centres, rows of the two calls): the fused matrix-core, fused low-d and rows families, the rows loop's
+# tiled form (d = 100, k = 64), and a shape km_pass sends to the wide-row screen while the allocation-free pass
+# runs the tiled rows loop over as few row blocks as its scratch holds (d = 768, k = 256)
+@pytest.mark.parametrize("d,k,ns", [(32, 64, (120_011, 33_007)), (4, 12, (120_011, 33_007)),
+                                    (16, 40, (120_011, 33_007)), (48, 100, (120_011, 33_007)),
+                                    (3, 300, (120_011, 33_007)), (100, 64, (50_011, 20_007)),
+                                    (768, 256, (20_011, 9_007))])
+def test_noalloc_pass_matches_km_pass(lib, d, k, ns):
     ctx = lib.Context()
-    for call, n in enumerate((120_011, 33_007)):
+    for call, n in enumerate(ns):
         X, C = _data(7 * d + k + call, n, d, k)
         say(f"[gpu] noalloc call {call} n={n} d={d} k={k}")
-        t1, l1, b1 = _noalloc(lib, ctx, X, C)
-        ref = lib.Context()
-        ref.set_parts([X])
-        t0, l0, b0 = ref.run_pass(C, labels=True, best=True)
-        ref.close()
-        assert np.array_equal(l1, l0), np.flatnonzero(l1 != l0)[:10]
-        assert np.array_equal(b1.view(np.uint32), b0.view(np.uint32))
-        assert np.array_equal(np.rint(t1[:, 0]), np.rint(t0[:, 0]))
-        fin = np.isfinite(t0)
-        assert np.array_equal(fin, np.isfinite(t1))
-        scale = np.maximum(np.abs(t0[fin]), 1.0)
-        assert np.all(np.abs(t1[fin] - t0[fin]) <= 1e-6 * scale)
+        _same(_noalloc(lib, ctx, X, C), _km_pass(lib, X, C))
+    ctx.close()
+
+
+def test_noalloc_back_to_back_on_one_stream(lib):
+    """Two calls queued on one stream without a synchronisation between them (the second smaller, another
+    family): the stream orders the second call's use of the scratch after the first's."""
+    ctx = lib.Context()
+    cases = [_data(101, 120_011, 32, 64), _data(102, 33_007, 4, 12)]
+    say("[gpu] noalloc back to back: 120011 x 32 k=64, then 33007 x 4 k=12")
+    got = _noalloc_calls(lib, ctx, cases)
+    for g, (X, C) in zip(got, cases):
+        _same(g, _km_pass(lib, X, C))
     ctx.close()
 
 
