@@ -121,6 +121,19 @@ int32_t km_seed_pp(km_ctx *ctx, int32_t k, const int64_t *sample, int64_t m, int
 int32_t km_pass_noalloc(km_ctx *ctx, const float *X, int64_t rows, int32_t dims, const float *C, int32_t k,
                         double *totals, uint32_t *labels, float *best, void *stream);
 
+/* Per-centre lower bounds between Lloyd passes (the reference's Elkan bounds, core.py:1690-2015). Exact passes on the
+ * wide-row path from 256 dims and 64 centres keep, per (row, centre), a float16 lower bound on the distance and per
+ * row an upper bound, and run a pass on them (exact scoring of only the centres a bound cannot rule out; the same
+ * labels and best, bit for bit) when a strided sample of 8192 rows says at most max_visited of the (row, centre)
+ * pairs need scoring - the reference's gate BOUNDS_MAX_VISITED (core.py:516, 2063-2106). km_bounds sets that
+ * fraction for ctx (default 0.05; 0 turns the bounds off and frees nothing until the data changes).
+ * km_bounds_info reports, since the data was set: passes tracked, passes run on the bounds, passes that wrote
+ * every row's bounds (the reference's build, core.py:2091-2096), and the sampled fraction of the last tracked pass
+ * (the reference's "visited", core.py:2010). Any pointer may be NULL. */
+int32_t km_bounds(km_ctx *ctx, double max_visited);
+int32_t km_bounds_info(km_ctx *ctx, int64_t *passes_tracked, int64_t *passes_on_bounds, int64_t *builds,
+                       double *last_fraction);
+
 /* Kernel timing with HIP events on the context's stream. km_profile(ctx, 1) clears and starts recording;
  * km_profile_read gives, for kernel id `kernel`, the summed milliseconds and launch count so far.
  * km_kernel_name(id) names an id ("" past the last); ids are stable within one build. */

@@ -110,6 +110,17 @@ struct km_ctx {
     DBuf<double> wd_part, wd_mu;    // mean / scatter partials; [mu (d), T] of the data set
     DBuf<double> pieces;            // the sums of clusters whose sorted rows span several chunks, per chunk
     DBuf<km_slice> wd_slices;       // the slice table on the device
+    // per-centre bounds between exact wide-row passes (km_bounds.hip): the float16 lower bounds (each slice's
+    // from bnd_off[i]), every row's upper bound and its centre, each centre's summed drift S, this pass's drift,
+    // the previous tracked pass's centres, and the device-side state (gates, sample count, counters)
+    DBuf<uint16_t> bnd_lb;
+    DBuf<float> bnd_ub, bnd_S, bnd_delta, bnd_Clast;
+    DBuf<uint32_t> bnd_ubl;
+    DBuf<km_bnd> bnd_st;
+    std::vector<int64_t> bnd_off;
+    bool bnd_valid = false;         // the device state describes this data and bnd_k
+    int bnd_k = 0;
+    double bnd_max_visited = 0.05;  // the reference's BOUNDS_MAX_VISITED (core.py:516); 0 turns the bounds off
     std::vector<km_slice> wd_slices_h;
     bool wd_ready = false;          // wd_mu and wd_slices describe the current data
     int64_t wd_limit = 0;           // the most changed rows a change-only pass takes
@@ -230,6 +241,7 @@ static void drop_parts(km_ctx *c) {
     c->n = 0;
     c->d = 0;
     c->wd_ready = false;
+    c->bnd_valid = false;
 }
 
 extern "C" void km_destroy(km_ctx *c) {
@@ -266,6 +278,13 @@ extern "C" void km_destroy(km_ctx *c) {
     c->pp_idx.release();
     c->pp_ws.release();
     c->wlab.release();
+    c->bnd_lb.release();
+    c->bnd_ub.release();
+    c->bnd_S.release();
+    c->bnd_delta.release();
+    c->bnd_Clast.release();
+    c->bnd_ubl.release();
+    c->bnd_st.release();
     c->wd_bcnt.release();
     c->wd_e.release();
     c->wd_H.release();
@@ -438,6 +457,62 @@ static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags
     return KM_OK;
 }
 
+// Per-centre bounds for this wide-row pass: offered to exact passes from KM_BND_MIN_DIMS dims and KM_BND_MIN_K
+// centres with packed keys, within KM_BND_MAX_BYTES of float16 bounds (the reference's _bounds_ok, core.py:1722-1724),
+// unless turned off. Sizes the state (a new data set or k starts it again) and queues the drift, the sample count and
+// the decision; returns whether the pass is tracked, with the sample stride.
+static int prepare_bounds(km_ctx *c, int k, int mode, const km_big_plan &bp0, const float *Cin, const int32_t *stop,
+                          bool *use, int64_t *tstride) {
+    *use = false;
+    if (c->bnd_max_visited <= 0.0 || mode != KM_EXACT || c->d < KM_BND_MIN_DIMS || k < KM_BND_MIN_K || bp0.ib <= 0)
+        return KM_OK;
+    int64_t tiles = 0, elems = 0;
+    std::vector<int64_t> off;
+    for (auto &p : c->parts) {
+        const int64_t t = (p.rows + 31) / 32;
+        off.push_back(elems);
+        tiles += t;
+        elems += t * bp0.nchunks * 1024;
+    }
+    if ((size_t)elems * sizeof(uint16_t) > KM_BND_MAX_BYTES) return KM_OK;
+    if (c->bnd_k != k || off != c->bnd_off) c->bnd_valid = false;
+    if (!c->bnd_valid) {
+        HIPCHK(c, c->bnd_lb.ensure((size_t)elems));
+        HIPCHK(c, c->bnd_ub.ensure((size_t)c->n));
+        HIPCHK(c, c->bnd_ubl.ensure((size_t)c->n));
+        HIPCHK(c, c->bnd_S.ensure((size_t)k));
+        HIPCHK(c, c->bnd_delta.ensure((size_t)k));
+        HIPCHK(c, c->bnd_Clast.ensure((size_t)k * c->d));
+        HIPCHK(c, c->bnd_st.ensure(1));
+        HIPCHK(c, hipMemsetAsync(c->bnd_st.p, 0, sizeof(km_bnd), c->stream));
+        c->bnd_off = off;
+        c->bnd_k = k;
+    }
+    *tstride = std::max<int64_t>(1, tiles / KM_BND_SAMPLE_TILES);
+    km_bnd *bs = c->bnd_st.p;
+    const float hi = km_bnd_hi(c->d);
+    HIPCHK(c, launch(c, KK_BOUNDS, [&] {
+        return km_launch_bnd_drift(Cin, c->bnd_Clast.p, k, c->d, c->bnd_valid ? 1 : 0, c->bnd_S.p, c->bnd_delta.p, bs,
+                                   stop, c->stream);
+    }));
+    int64_t row0 = 0;
+    for (size_t i = 0; i < c->parts.size(); i++) {
+        const Part &p = c->parts[i];
+        HIPCHK(c, launch(c, KK_BOUNDS, [&] {
+            return km_launch_bnd_count(c->bnd_lb.p + c->bnd_off[i], c->bnd_ub.p + row0, c->bnd_ubl.p + row0, p.rows, k,
+                                       bp0.nchunks, *tstride, c->bnd_S.p, c->bnd_delta.p, hi, bs, stop, c->dev.cus,
+                                       c->stream);
+        }));
+        row0 += p.rows;
+    }
+    HIPCHK(c, launch(c, KK_BOUNDS, [&] {
+        return km_launch_bnd_decide(bs, c->bnd_max_visited, c->bnd_S.p, k, stop, c->stream);
+    }));
+    c->bnd_valid = true;
+    *use = true;
+    return KM_OK;
+}
+
 // The wide-row pass: centre operands, then per slice the screen + exact rescoring (labels and best for every
 // row), then per slice the sorted accumulation into one range sum per slice, then the finish. In the fit loop
 // (lmode set) the labels alternate between two arrays by pass parity; a KM_LSTATE_DELTA pass counts the rows that
@@ -500,6 +575,13 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     float *best_all = best_d ? best_d : c->best.p;
     // without per-row outputs, single-candidate rows skip the rescoring and the accumulation adds the distances
     const int lite = (labels_d || best_d) ? 0 : 1;
+    bool bnd = false;
+    int64_t tstride = 1;
+    {
+        const int r = prepare_bounds(c, k, mode, bp0, Cin, stop, &bnd, &tstride);
+        if (r) return r;
+    }
+    km_bnd *bs = bnd ? c->bnd_st.p : nullptr;
     HIPCHK(c, launch(c, KK_BIG_PREP, [&] {
         return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop, c->stream);
     }));
@@ -512,13 +594,33 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
                 return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop,
                                              c->stream);
             }));
+        // a tracked pass: the plain screen, the bound-writing screen and the bounds list are all queued, and the
+        // decision on the device lets the ones this pass needs run
         HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
             return km_launch_big_screen(bp, mode, p.x16, p.xsq, c->xmax.p, p.rows, d, c->cop.p, c->bmax.p, k,
-                                        c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl, stop, c->stream);
+                                        c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl,
+                                        bnd ? &bs->skip_plain : stop, c->stream);
         }));
+        km_bnd_refresh bref{};
+        if (bnd) {
+            uint16_t *lb = c->bnd_lb.p + c->bnd_off[i];
+            bref = km_bnd_refresh{lb, c->bnd_ub.p + row0, c->bnd_ubl.p + row0, c->bnd_S.p, bp.nchunks,
+                                  km_bnd_lo(d) * (1.0f - 0x1p-21f), km_bnd_hi(d) * (1.0f + 0x1p-21f), bs};
+            HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
+                return km_launch_big_screen_bnd(bp, p.x16, p.xsq, p.rows, d, c->cop.p, c->bmax.p, k, c->ncand.p,
+                                                c->cand.p, c->over.p, c->multi.p, c->ctl, lb, bref.ub, bref.ubl,
+                                                tstride, bs, c->dev.cus, c->stream);
+            }));
+            HIPCHK(c, launch(c, KK_BOUNDS, [&] {
+                return km_launch_bnd_list(lb, bref.ub, bref.ubl, p.rows, k, bp.nchunks, c->bnd_S.p, c->bnd_delta.p,
+                                          km_bnd_hi(d), c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl, bs,
+                                          c->dev.cus, c->stream);
+            }));
+        }
         HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {
             return km_launch_big_rescore(p.X, p.rows, d, Cin, k, c->ncand.p, c->cand.p, c->over.p, c->multi.p,
-                                         c->ctl, lab_all + row0, best_all + row0, lite, c->okeys.p, stop, c->stream);
+                                         c->ctl, lab_all + row0, best_all + row0, lite, c->okeys.p, stop, c->stream,
+                                         bnd ? &bref : nullptr);
         }));
         row0 += p.rows;
     }
@@ -1174,6 +1276,32 @@ extern "C" int32_t km_pass_noalloc(km_ctx *c, const float *X, int64_t rows, int3
         HIPCHK(c, hipGetLastError());
     }
     c->last_path = family_path(fam);
+    return KM_OK;
+}
+
+// ------------------------------------------------------------------ per-centre bounds
+
+extern "C" int32_t km_bounds(km_ctx *c, double max_visited) {
+    if (!c) return KM_EINVAL;
+    if (!(max_visited >= 0.0 && max_visited <= 1.0))
+        return fail(c, KM_EINVAL, "max_visited must be a fraction in [0, 1], got %g", max_visited);
+    c->bnd_max_visited = max_visited;
+    return KM_OK;
+}
+
+extern "C" int32_t km_bounds_info(km_ctx *c, int64_t *passes_tracked, int64_t *passes_on_bounds, int64_t *builds,
+                                  double *last_fraction) {
+    if (!c) return KM_EINVAL;
+    km_bnd st{};
+    if (c->bnd_valid && c->bnd_st.p) {
+        HIPCHK(c, hipSetDevice(c->device));
+        HIPCHK(c, hipMemcpyAsync(&st, c->bnd_st.p, sizeof st, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+    }
+    if (passes_tracked) *passes_tracked = (int64_t)st.n_tracked;
+    if (passes_on_bounds) *passes_on_bounds = (int64_t)st.n_bounds;
+    if (builds) *builds = (int64_t)st.n_builds;
+    if (last_fraction) *last_fraction = c->bnd_valid ? st.last_frac : 1.0;
     return KM_OK;
 }
 

@@ -257,29 +257,34 @@ __global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C
 // The wave's 32 rows stay in registers as B operands (4 per K-step): up to 48 K-steps two blocks share a CU (256
 // registers a wave); above that one block does, and the 512 registers of a lone wave per SIMD (accumulation
 // registers included, which the matrix cores read operands from) hold up to 96 K-steps without spilling.
-template <int DS, bool PACK>
-__global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
-    const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
+// What the bound-writing instance writes besides the screen's own outputs (the per-centre bounds between passes,
+// km_bounds.hip): per row ub / ubl (an upper bound, hi-scaled, on the distance to the screen minimiser, and that
+// centre), and with wlb this tile's float16 lower bounds sqrt(|x|^2 + a'_c - E) lo, rounded toward zero.
+struct kb_bnd_out {
+    uint16_t *lb;
+    float *ub;
+    uint32_t *ubl;
+    float lo, hi;
+    bool lists;   // also the candidate lists (a tile the plain screen does not take this pass)
+};
+
+// One 32-row tile per wave (tile >= ntiles: a wave of zero rows that only takes part in the block's barriers).
+template <int DS, bool PACK, bool BND>
+__device__ __forceinline__ void kb_screen_tile(
+    int64_t tile, const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
-    int approx, const uint32_t *__restrict__ xmax, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand,
-    uint32_t *__restrict__ over, uint32_t *__restrict__ multi, km_control *__restrict__ ctl,
-    const int32_t *__restrict__ stop) {
+    int approx, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
+    uint32_t *__restrict__ multi, km_control *__restrict__ ctl, const kb_bnd_out &bnd) {
     constexpr int DP = 16 * DS, AK = DS + 1, NACC = DP + 2;
     constexpr float GACC = (float)(2.04 * kb_gamma(NACC) * (1.0 + 0x1p-20));
     constexpr float GAM2 = (float)((1.01 * kb_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
     constexpr float FLUSH = (float)0x1p-119;
     constexpr float TINY = (float)((DP + 2) * 0x1p-118);
-    if (stop && *stop) return;
-    // Approximate mode only while this pass's centres pass the reference's half-precision guard (core.py:1055-1058):
-    // sqrt(max |x|^2 max |c|^2) < 65504 / 4, from the data's largest |x|^2 (rounded up, +inf if any row is not
-    // finite) and the largest |c|^2 of the centres. Otherwise the pass is exact.
-    if (approx) approx = sqrt((double)kb_f32(*xmax) * (double)maxes[1]) < KB_APPROX_LIMIT;
     extern __shared__ float lds[];
     char *ring = reinterpret_cast<char *>(lds);   // two slices of at most kb_slice(DS) K-steps, 1 KB each
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int h = lane >> 5;
     const int64_t ntiles = (n + 31) / 32;
-    const int64_t tile = (int64_t)blockIdx.x * KB_WAVES + wave;
     const bool have = tile < ntiles;
     const int64_t row = tile * 32 + (lane & 31);
     const bool real_row = have && row < n;
@@ -369,6 +374,15 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
     const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
     const float E = (2.0f * exn * cnmax + nx * fmax + exn * fmax) * (1.0f + 0x1p-20f) + GACC * nx * cnmax +
                     GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
+    // Bound-writing instance: D_c >= |x|^2 + a'_c - E. With |x|^2 >= xsq_up (1 - 2^-18) and every |a'_c| at most
+    // max|c|^2 + 2 |x| max|c| + E, the slack 2^-21 (|x|^2 + E + max |a'|) covers the float32 additions, so
+    // lbase + a'_c (as computed) is at most D_c.
+    float lbase = 0.0f;
+    if (BND) {
+        const float xlo = xsq_up * (1.0f - 0x1p-18f);
+        const float amax = csqmax + 2.0f * nx * cnmax + E;
+        lbase = (xlo - E) - 0x1p-21f * (xlo + E + amax);
+    }
     // a key bound Tp with key <= Tp whenever key - rho |key| <= T
     auto key_bound = [&](float m) {
         const float akm = m + rho * fabsf(m);
@@ -404,6 +418,18 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
             // read it must be compiled code, whose hazard tracking inserts the wait states an MFMA result needs
             // (inline assembly here read stale accumulators)
             m1 = PACK ? kb_min(m1, key[v]) : fminf(m1, key[v]);
+        }
+        if (BND && have) {   // this chunk's lower bounds, 32 contiguous bytes per lane
+            uint32_t pk[8];
+#pragma unroll
+            for (int v = 0; v < 16; v += 2) {
+                const float a0 = fminf(__builtin_sqrtf(fmaxf(lbase + acc[v], 0.0f)) * bnd.lo, 65504.0f);
+                const float a1 = fminf(__builtin_sqrtf(fmaxf(lbase + acc[v + 1], 0.0f)) * bnd.lo, 65504.0f);
+                pk[v / 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a0, a1));
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(bnd.lb + ((tile * nchunks + ch) * 64 + lane) * 16);
+            dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
         }
         if (approx) continue;
         const float mrow = kb_min(m1, kb_partner(m1, lane));
@@ -446,7 +472,7 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
         int w = 0;
         for (int q = 0; q < cnt; q++) {
             const float kq = list[q * 64];
-            if (kq <= Tp)
+            if (kq <= Tp && (!BND || bnd.lists))
                 cand[row * KB_CAP + h * KB_HALF + (w++)] = PACK ? (uint16_t)(kb_u32(kq) & IMASK) : lidx[q * 64];
         }
         cnt = w;
@@ -458,6 +484,16 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
     const int cnt_o = (int)kb_f32u(kb_partner(kb_u32f((uint32_t)(spill ? KB_HALF + 1 : cnt)), lane));
     const bool spill_o = cnt_o > KB_HALF;
     if (h != 0) return;
+    if (BND) {   // an upper bound on the distance to the minimiser m (D_m <= |x|^2 + a'_m + E), and m
+        float u = INFINITY;
+        if (finite) {
+            const float dm_up = fmaxf(0.0f, xsq_up + (m1 + rho * fabsf(m1)) + E) * (1.0f + 0x1p-20f);
+            u = __builtin_sqrtf(dm_up) * bnd.hi;
+        }
+        bnd.ub[row] = u < INFINITY ? u : INFINITY;
+        bnd.ubl[row] = kb_u32(m1) & IMASK;
+        if (!bnd.lists) return;
+    }
     int code;
     if (!finite) {
         code = KB_OVER;   // non-finite data: the rows loop decides
@@ -483,6 +519,49 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
     }
 }
 
+template <int DS, bool PACK>
+__global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
+    const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
+    const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
+    int approx, const uint32_t *__restrict__ xmax, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand,
+    uint32_t *__restrict__ over, uint32_t *__restrict__ multi, km_control *__restrict__ ctl,
+    const int32_t *__restrict__ stop) {
+    if (stop && *stop) return;
+    // Approximate mode only while this pass's centres pass the reference's half-precision guard (core.py:1055-1058):
+    // sqrt(max |x|^2 max |c|^2) < 65504 / 4, from the data's largest |x|^2 (rounded up, +inf if any row is not
+    // finite) and the largest |c|^2 of the centres. Otherwise the pass is exact.
+    if (approx) approx = sqrt((double)kb_f32(*xmax) * (double)maxes[1]) < KB_APPROX_LIMIT;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb_screen_tile<DS, PACK, false>((int64_t)blockIdx.x * KB_WAVES + wave, X16T, xsq, n, d, Cop, maxes, k, nchunks,
+                                    ib, rho, approx, ncand, cand, over, multi, ctl, kb_bnd_out{});
+}
+
+// The bound-writing screen of a tracked exact pass (packed keys): the sample tiles (t % tstride == 0), bounds only
+// (the plain screen lists their candidates), or every tile, bounds and lists, when the pass builds (the plain screen
+// then stands down); a grid of blocks loops over them (a pass that writes only the sample keeps most blocks idle, at
+// no more cost than their launch).
+template <int DS>
+__global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen_bnd(
+    const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
+    const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
+    uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
+    uint32_t *__restrict__ multi, km_control *__restrict__ ctl, uint16_t *__restrict__ lb, float *__restrict__ ub,
+    uint32_t *__restrict__ ubl, float lo, float hi, int64_t tstride, const km_bnd *__restrict__ bs) {
+    if (bs->skip_bscreen) return;
+    const bool all = bs->build != 0;
+    const int64_t ntiles = (n + 31) / 32;
+    const int64_t step = all ? 1 : tstride;
+    const int64_t nwork = (ntiles + step - 1) / step;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const kb_bnd_out out{lb, ub, ubl, lo, hi, all};
+    for (int64_t wb = blockIdx.x; wb * KB_WAVES < nwork; wb += gridDim.x) {   // block-uniform
+        __syncthreads();   // every wave is done with the previous tile's A slices before the ring is refilled
+        const int64_t w = wb * KB_WAVES + wave;
+        kb_screen_tile<DS, true, true>(w < nwork ? w * step : ntiles, X16T, xsq, n, d, Cop, maxes, k, nchunks, ib,
+                                       rho, 0, ncand, cand, over, multi, ctl, out);
+    }
+}
+
 // ------------------------------------------------------------------ exact rescoring
 
 // Block (256 threads) per 64 consecutive rows. Each (row, candidate) pair is a work item, items ordered by row and
@@ -505,8 +584,11 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                                                        const uint32_t *__restrict__ list,
                                                        const km_control *__restrict__ ctl,
                                                        uint32_t *__restrict__ labels, float *__restrict__ best,
-                                                       const int32_t *__restrict__ stop) {
+                                                       const int32_t *__restrict__ stop, km_bnd_refresh bref) {
     if (stop && *stop) return;
+    // with per-centre bounds that describe every tile: each item's exact distance refreshes its bound, and each
+    // row's result its upper bound (block-uniform)
+    const bool refresh = bref.lb && bref.bs->built;
     __shared__ uint32_t rid[KB_RR];   // the block's rows: consecutive, or entries of the list
     __shared__ float xs[KB_RR * (KB_RCH + 1)];
     __shared__ float cs[KB_RT * (KB_RCH + 1)];
@@ -669,6 +751,25 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         }
         labels[rid[tid]] = bl;
         best[rid[tid]] = bst;
+        if (refresh) {
+            const float u = (bst >= 0.0f && bst < INFINITY) ? __builtin_sqrtf(bst) * bref.hi : INFINITY;
+            bref.ub[rid[tid]] = u < INFINITY ? u : INFINITY;
+            bref.ubl[rid[tid]] = bl;
+        }
+    }
+    if (refresh) {
+        // lb_c = sqrt(s_c) lo + S_c (frame), rounded toward zero: s_c <= D_c (1 + g), so sqrt(s_c) lo is at most
+        // sqrt(D_c) (1 - g); 1 - 2^-22 covers the float32 addition. A non-finite distance or drift writes 0.
+        for (int q = tid; q < items; q += KB_RT) {
+            const int64_t r = rid[it_r[q]];
+            const int c = it_c[q];
+            const float sq = it_s[q], sc = bref.S[c];
+            float v = 0.0f;
+            if (sc < INFINITY && sq >= 0.0f)
+                v = sq < INFINITY ? fminf((__builtin_sqrtf(sq) * bref.lo + sc) * (1.0f - 0x1p-22f), 65504.0f) : 65504.0f;
+            const uint32_t hv = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(v, 0.0f));
+            bref.lb[km_bnd_index(r, c, bref.nchunks)] = (uint16_t)hv;
+        }
     }
     }
 }
@@ -1103,37 +1204,81 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
                                  uint32_t *labels, float *best, int lite, uint64_t *okeys, const int32_t *stop,
-                                 hipStream_t s) {
+                                 hipStream_t s, const km_bnd_refresh *bref) {
     const bool v4 = (d % 4 == 0) && ((uintptr_t)X % 16 == 0) && ((uintptr_t)C % 16 == 0);
     const unsigned chunks = (unsigned)((n + KB_RR - 1) / KB_RR);
+    const km_bnd_refresh br = bref ? *bref : km_bnd_refresh{};
     hipError_t e;
     typedef void (*rescore_fn)(const float *, int64_t, int, const float *, int, const uint16_t *, const uint16_t *,
-                               const uint32_t *, const km_control *, uint32_t *, float *, const int32_t *);
+                               const uint32_t *, const km_control *, uint32_t *, float *, const int32_t *,
+                               km_bnd_refresh);
     if (lite) {
         hipLaunchKernelGGL(k_big_label1, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ncand, cand, n, labels,
                            stop);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         const rescore_fn fn = v4 ? k_big_rescore<true, true> : k_big_rescore<false, true>;
         hipLaunchKernelGGL(fn, dim3(chunks < 4096u ? chunks : 4096u), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
-                           multi, ctl, labels, best, stop);
+                           multi, ctl, labels, best, stop, br);
     } else {
         const rescore_fn fn = v4 ? k_big_rescore<true, false> : k_big_rescore<false, false>;
         hipLaunchKernelGGL(fn, dim3(chunks), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand, (const uint32_t *)nullptr,
-                           ctl, labels, best, stop);
+                           ctl, labels, best, stop, br);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (k <= KB_FSPLIT || !okeys) {
         hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, (int64_t)0, ctl, labels,
                            best, (uint64_t *)nullptr, stop);
-        return hipGetLastError();
+    } else {
+        hipLaunchKernelGGL(k_big_fkeys_init, dim3(256), dim3(256), 0, s, okeys, ctl, stop);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, (int64_t)0, ctl, labels,
+                           best, okeys, stop);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_big_fkeys_fin, dim3(256), dim3(256), 0, s, okeys, over, ctl, labels, best, stop);
     }
-    hipLaunchKernelGGL(k_big_fkeys_init, dim3(256), dim3(256), 0, s, okeys, ctl, stop);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_fullscan, dim3(1024), dim3(256), 0, s, X, d, C, k, over, (int64_t)0, ctl, labels, best,
-                       okeys, stop);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_big_fkeys_fin, dim3(256), dim3(256), 0, s, okeys, over, ctl, labels, best, stop);
+    if (!br.lb) return hipSuccess;
+    return km_launch_bnd_overfix(over, ctl, labels, best, br.ub, br.ubl, br.hi, br.bs, stop, s);
+}
+
+template <int DS>
+static hipError_t kb_launch_screen_bnd(const km_big_plan &pl, const uint16_t *X16T, const float *xsq, int64_t n, int d,
+                                       const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand,
+                                       uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
+                                       uint16_t *lb, float *ub, uint32_t *ubl, int64_t tstride, km_bnd *bs, int cus,
+                                       hipStream_t s) {
+    const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
+    const int ak = DS + 1, spc = (ak + kb_slice(DS) - 1) / kb_slice(DS), slk = (ak + spc - 1) / spc;
+    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * KB_HALF * 64 * 4;
+    if (lds > 65536) {
+        hipError_t e = hipFuncSetAttribute((const void *)k_big_screen_bnd<DS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    // one round of blocks on the device (one or two per CU), each looping over its tiles
+    const int64_t want = (pl.ntiles + KB_WAVES - 1) / KB_WAVES;
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)cus * (DS > 48 ? 1 : 2)));
+    hipLaunchKernelGGL(k_big_screen_bnd<DS>, dim3((unsigned)blocks), dim3(64 * KB_WAVES), lds, s, X16T, xsq, n, d,
+                       Cop, maxes, k, pl.nchunks, pl.ib, rho, ncand, cand, over, multi, ctl, lb, ub, ubl,
+                       km_bnd_lo(d) * (1.0f - 0x1p-21f), km_bnd_hi(d) * (1.0f + 0x1p-21f), tstride, bs);
     return hipGetLastError();
+}
+
+hipError_t km_launch_big_screen_bnd(const km_big_plan &pl, const uint16_t *X16T, const float *xsq, int64_t n, int d,
+                                    const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
+                                    uint32_t *over, uint32_t *multi, km_control *ctl, uint16_t *lb, float *ub,
+                                    uint32_t *ubl, int64_t tstride, km_bnd *bs, int cus, hipStream_t s) {
+    if (pl.ib <= 0) return hipErrorInvalidValue;   // packed keys only (k <= KM_BIG_PACK_MAX_K)
+    switch (pl.DS) {
+        case 16: return kb_launch_screen_bnd<16>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 24: return kb_launch_screen_bnd<24>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 32: return kb_launch_screen_bnd<32>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 48: return kb_launch_screen_bnd<48>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 60: return kb_launch_screen_bnd<60>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 64: return kb_launch_screen_bnd<64>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 96: return kb_launch_screen_bnd<96>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t km_launch_rows_tiled(const float *X, int64_t n, int d, const float *C, int k, uint32_t *labels, float *best,

@@ -69,6 +69,7 @@ enum km_kernel_id {
     KK_SEED_PP,
     KK_RELOCATE,
     KK_CHANGE,   // the wide-row fit loop's change count, gate and change-only sums
+    KK_BOUNDS,   // the per-centre bounds: drift, sample count, decision, candidate lists
     KK_COUNT
 };
 extern const char *const km_kernel_names[KK_COUNT];
@@ -248,12 +249,85 @@ hipError_t km_launch_rows_tiled(const float *X, int64_t n, int d, const float *C
 hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *C, int k, const uint16_t *ncand,
                                  const uint16_t *cand, const uint32_t *over, const uint32_t *multi, km_control *ctl,
                                  uint32_t *labels, float *best, int lite, uint64_t *okeys, const int32_t *stop,
-                                 hipStream_t s);
+                                 hipStream_t s, const struct km_bnd_refresh *bref = nullptr);
 // C_lite non-null: the best column is the rows' FMA-form distances to C, not best[] (pair with a lite rescore)
 hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n, int d, const uint32_t *labels,
                                const float *best, const float *C_lite, int k, uint32_t *H, uint32_t *counts,
                                uint32_t *base, uint32_t *perm, double *pieces, double *tmp, const int32_t *stop,
                                hipStream_t s);
+// ---- per-centre lower bounds between passes (km_bounds.hip; the reference's Elkan bounds, core.py:1690-2015)
+//
+// For exact wide-row passes from KM_BND_MIN_DIMS dims: one float16 lower bound per (row, centre) on the distance
+// |x - c| (not squared), kept between passes in a frame: the stored value less S_c, the centre's summed drift since
+// the frame began, bounds sqrt(D_c) (1 - g) from below (g: the direct form's relative error). Per row an upper
+// bound ub >= sqrt(D_l) (1 + g) on the distance to one centre l (ubl), raised by l's drift each pass. A pass on
+// the bounds scores exactly only the centres whose bound is not above ub (the rows loop's label is always one of
+// them), through the same candidate lists the screen fills.
+// Layout of the bounds, tile-major like the screen's registers: km_bnd_index(row, c, nchunks).
+#define KM_BND_MIN_DIMS 256          // the reference's BOUNDS_MIN_DIMS (core.py:513)
+#define KM_BND_MIN_K 64              // the reference's TILES_MIN_K, which _bounds_ok requires (core.py:1722-1724)
+#define KM_BND_MAX_BYTES ((size_t)16 << 30)   // the reference's BOUNDS_MAX_BYTES (core.py:515)
+#define KM_BND_SAMPLE_TILES 256      // 32-row tiles the gate samples: the reference's BOUNDS_SAMPLE_ROWS (8192)
+__host__ __device__ inline int64_t km_bnd_index(int64_t row, int c, int nchunks) {
+    const int ch = c >> 5, cc = c & 31;
+    const int h = (cc >> 2) & 1, v = ((cc >> 3) << 2) | (cc & 3);
+    return (((row >> 5) * nchunks + ch) * 64 + (row & 31) + 32 * h) * 16 + v;
+}
+// centre held at value v of half h of chunk ch (the screen's accumulator order)
+__host__ __device__ inline int km_bnd_centre(int ch, int h, int v) { return 32 * ch + 8 * (v >> 2) + 4 * h + (v & 3); }
+
+struct km_bnd {
+    int32_t skip_plain;    // nonzero: the plain screen stands down (bounds, a build, or the loop stopped)
+    int32_t skip_bscreen;  // nonzero: the bound-writing screen stands down (bounds, or the loop stopped)
+    int32_t skip_list;     // nonzero: the bounds list stands down (a screened pass, or the loop stopped)
+    int32_t build;         // this pass writes every tile's bounds (else the sample tiles' only)
+    int32_t sample_ok;     // the sample tiles' bounds describe the previous tracked pass
+    int32_t built;         // every tile's bounds do (refreshes are worth writing)
+    unsigned long long visits;     // sampled (row, centre) pairs this pass would visit, the ub centre excluded
+    unsigned long long pairs;      // sampled (row, centre) pairs
+    unsigned long long n_bounds;   // passes run on the bounds
+    unsigned long long n_builds;   // passes that wrote every tile's bounds
+    unsigned long long n_tracked;  // tracked passes
+    double last_frac;              // the sampled fraction at the last tracked pass
+};
+// The bounds' slack factors for rows of d dims: lo <= 1 - g, hi >= 1 + g beyond float32 rounding
+float km_bnd_lo(int d);
+float km_bnd_hi(int d);
+// Per pass, before the screen: each centre's drift |C - Clast| (rounded up) into delta and S (valid = 0 starts a
+// new state: S = 0, nothing sampled, nothing built); Clast = C.
+hipError_t km_launch_bnd_drift(const float *C, float *Clast, int k, int d, int valid, float *S, float *delta,
+                               km_bnd *bs, const int32_t *stop, hipStream_t s);
+// The sampled count of one slice (tiles t with t % tstride == 0), then (once) the decision and the gates.
+hipError_t km_launch_bnd_count(const uint16_t *lb, const float *ub, const uint32_t *ubl, int64_t n, int k,
+                               int nchunks, int64_t tstride, const float *S, const float *delta, float hi,
+                               km_bnd *bs, const int32_t *stop, int cus, hipStream_t s);
+hipError_t km_launch_bnd_decide(km_bnd *bs, double max_visited, float *S, int k, const int32_t *stop, hipStream_t s);
+// A pass on the bounds, one slice: candidate lists (ncand/cand/over/multi as the screen writes them) and every
+// row's raised ub; gated on bs->skip_list.
+hipError_t km_launch_bnd_list(const uint16_t *lb, float *ub, const uint32_t *ubl, int64_t n, int k, int nchunks,
+                              const float *S, const float *delta, float hi, uint16_t *ncand, uint16_t *cand,
+                              uint32_t *over, uint32_t *multi, km_control *ctl, km_bnd *bs, int cus, hipStream_t s);
+// After the full scan of a slice's overflow rows: their ub from the exact best (when bs->built).
+hipError_t km_launch_bnd_overfix(const uint32_t *over, const km_control *ctl, const uint32_t *labels,
+                                 const float *best, float *ub, uint32_t *ubl, float hi, const km_bnd *bs,
+                                 const int32_t *stop, hipStream_t s);
+// Bound-writing screen (one slice): the screen with every row's ub / ubl and the float16 bounds of the sample
+// tiles (t % tstride == 0), or of every tile when bs->build; gated on bs->skip_bscreen.
+struct km_big_plan;
+hipError_t km_launch_big_screen_bnd(const km_big_plan &pl, const uint16_t *X16T, const float *xsq, int64_t n, int d,
+                                    const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
+                                    uint32_t *over, uint32_t *multi, km_control *ctl, uint16_t *lb, float *ub,
+                                    uint32_t *ubl, int64_t tstride, km_bnd *bs, int cus, hipStream_t s);
+// Refreshes the rescoring and the overflow fix write (null: none): the bounds of a slice, S, lo/hi
+struct km_bnd_refresh {
+    uint16_t *lb;        // the slice's bounds
+    float *ub;           // the slice's upper bounds
+    uint32_t *ubl;
+    const float *S;
+    int nchunks;
+    float lo, hi;
+    const km_bnd *bs;    // refreshes only when bs->built
+};
 // ---- per-cluster sums over rows listed in cluster order, in fixed chunks (km_chunks.hip)
 #define KM_CHUNK_MAX_DIMS 1536
 // pieces for npos listed positions: mode 0 (rows, best[] column) and 1 (rows, distances to C), mode 2 (change

@@ -45,6 +45,8 @@ SIGNATURES = [
     ("km_stream_probe", _c.c_int32, [_c.c_void_p, _c.c_int64, _c.c_int32, _f64p]),
     ("km_pass_noalloc", _c.c_int32, [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int32, _c.c_void_p, _c.c_int32,
                                      _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p]),
+    ("km_bounds", _c.c_int32, [_c.c_void_p, _c.c_double]),
+    ("km_bounds_info", _c.c_int32, [_c.c_void_p, _i64p, _i64p, _i64p, _f64p]),
 ]
 
 _lib = None
@@ -168,6 +170,20 @@ class Context:
         self._check(lib().km_seed_pp(self._h, int(k), _ptr(sample, ctypes.c_int64), sample.shape[0], int(first),
                                      _ptr(seeds, ctypes.c_uint64), _ptr(out, ctypes.c_float)))
         return out
+
+    # ---- per-centre bounds (the reference's Elkan bounds, core.py:1690-2015)
+    def bounds(self, max_visited):
+        """Sets the gate of the bounds path: a pass runs on the bounds while a sample says at most this fraction
+        of (row, centre) pairs needs scoring (the reference's BOUNDS_MAX_VISITED); 0 turns them off."""
+        self._check(lib().km_bounds(self._h, float(max_visited)))
+
+    def bounds_info(self):
+        """-> dict(tracked, on_bounds, builds, last_fraction) since the data was set."""
+        t, b, u = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        f = ctypes.c_double()
+        self._check(lib().km_bounds_info(self._h, ctypes.byref(t), ctypes.byref(b), ctypes.byref(u),
+                                         ctypes.byref(f)))
+        return {"tracked": t.value, "on_bounds": b.value, "builds": u.value, "last_fraction": f.value}
 
     # ---- timing and diagnostics
     def profile(self, enable=True):

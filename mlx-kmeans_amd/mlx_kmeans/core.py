@@ -25,6 +25,11 @@ SLICE_ROWS = 100_000_000                # rows per slice that KMeans cuts its in
 PART_MAX_ELEMENTS = 2**32 - 1           # elements per slice: the reference's limit (its kernels' uint32 offsets),
                                         # refused above it as the reference does (core.py:2028-2032)
 
+# Per-centre bounds between passes (core.py:1690-2015): exact wide-row passes from 256 dims and 64 centres keep a
+# lower bound per (row, centre) and run on them while a sample of 8192 rows says at most this fraction of the
+# pairs needs scoring (the reference's BOUNDS_MAX_VISITED, core.py:516). Read at every pass; 0 turns them off.
+BOUNDS_MAX_VISITED = 0.05
+
 # the reference's `method` names -> this engine's paths. "rows" is the direct-form scan; the matrix-core screen
 # plays the part of the reference's "tiles"/"tiles1"; the others are reference-internal variants that map onto
 # the automatic choice. Every path returns the same labels.
@@ -114,9 +119,12 @@ def _context(parts, C, method="auto"):
         raise ValueError(f"data has {d} columns but the centers have {C.shape[1]}; "
                          f"fit and predict need the same features")
     path = _path(method, C.shape[0], d)
-    if dd is not None:
-        return dd, False, path
-    return DeviceData(parts), True, path
+    if dd is None:
+        dd, owned = DeviceData(parts), True
+    else:
+        owned = False
+    dd.ctx.bounds(BOUNDS_MAX_VISITED)
+    return dd, owned, path
 
 
 def _path(method, k, d):
@@ -184,7 +192,8 @@ def kmeans_pp_init(parts, rows, k, rng, sample=None):
 def _gpu_pass(parts, C, method="auto", accumulate="auto", iterate=False):
     """One exact assignment pass -> (float64 totals (k, d+2) [count, inertia, sums...], [(labels u32, best f32)]
     per slice). core.py:2018-2197. `accumulate` is accepted for compatibility: every accumulation here is
-    deterministic and compensated. `iterate` is accepted and has no effect (no per-dataset state is kept)."""
+    deterministic and compensated. `iterate` is accepted and has no effect: a DeviceData keeps its per-centre
+    bounds across every kind of pass (each pass's labels and best are the rows loop's either way)."""
     del accumulate, iterate
     dd, owned, path = _context(parts, C, method)
     try:

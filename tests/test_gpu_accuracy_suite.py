@@ -7,11 +7,11 @@ float32 resolution, counts exact, centres within 1e-6 of the data's RMS, inertia
 higher: labels and best equal the oracle's rows loop (core.py:263-274) bit for bit, on every path that serves the
 shape. The relocation sequences (accuracy.py:294-303, 130-169) take eight Lloyd steps each, every step against
 the float64 step (accuracy.py:108-129) on the step's own labels and, where one cluster empties, against
-scikit-learn's lloyd. The bounds sequences (accuracy.py:305-318, 171-245) drive the reference's per-centre
-bounds, which this engine does not keep; their inputs run here as the same sequences of exact Lloyd steps (a
-restart at step 6, three slices, relocation, a column at 1e-6 scale), each step held to the same bar, and the
-centres past float16 range (accuracy.py:218-245) as one pass after five steps (the reference takes as many
-steps as its bounds predictor needs before it plants them).
+scikit-learn's lloyd. The bounds sequences (accuracy.py:305-318, 171-245) drive the per-centre bounds: the same
+sequences of exact Lloyd steps (a restart at step 6, three slices, relocation, a column at 1e-6 scale), each step
+held to the same bar, and, as the reference asserts (accuracy.py:209), at least a third of the steps run on the
+bounds. The centres past float16 range (accuracy.py:218-245) are planted after five steps, with the gate at 0.5
+as the reference sets it there, so that the pass runs on bounds a float16 cannot hold for that centre.
 """
 import os
 import sys
@@ -212,7 +212,8 @@ def test_single_pass_cases(lib, name):
 
 def _steps(lib, X, C0, steps, slice_rows=None, inject=None, sample=None, full_at=None, sklearn=False):
     """Lloyd steps from C0; each step's labels bit for bit against the oracle (on `sample` seeded rows when given),
-    its centres within 1e-6 of the float64 step on the same labels -> (empties relocated, steps checked)."""
+    its centres within 1e-6 of the float64 step on the same labels -> (empties relocated, steps whose Lloyd step ran
+    on the per-centre bounds)."""
     import oracle
     ctx = lib.Context()
     ctx.set_parts(_parts(X, slice_rows))
@@ -220,7 +221,7 @@ def _steps(lib, X, C0, steps, slice_rows=None, inject=None, sample=None, full_at
     rows = None
     if sample:
         rows = np.sort(np.random.default_rng(5).choice(len(X), sample, replace=False))
-    C, empties = C0.copy(), 0
+    C, empties, on_bounds = C0.copy(), 0, 0
     for step in range(steps):
         if inject is not None and step == inject[0]:
             C = inject[1]
@@ -229,7 +230,11 @@ def _steps(lib, X, C0, steps, slice_rows=None, inject=None, sample=None, full_at
         _check_labels(X, C, labels, best, rows)
         if full_at is None or step in full_at:
             _check_suite_bar(X, C, labels, tot)
+        before = ctx.bounds_info()["on_bounds"]
         ours, _, n_empty = ctx.lloyd_step(C)
+        info = ctx.bounds_info()
+        on_bounds += info["on_bounds"] > before
+        say(f"[gpu]     bounds: {info}")
         ref, ref_empty = oracle.reference_lloyd_step(X, C, labels)
         assert n_empty == ref_empty
         err = float(np.max(np.abs(ours.astype(np.float64) - ref))) / scale
@@ -245,14 +250,14 @@ def _steps(lib, X, C0, steps, slice_rows=None, inject=None, sample=None, full_at
         empties += n_empty
         C = ours
     ctx.close()
-    return empties
+    return empties, on_bounds
 
 
 @pytest.mark.parametrize("name", RELOC)
 def test_relocation_sequences(lib, name):
     c = case(name)
     say(f"[gpu] accuracy suite {name}: {c['X'].shape}, k = {len(c['C'])}")
-    empties = _steps(lib, c["X"], c["C"], 8, sklearn=c.get("sklearn", False))
+    empties, _ = _steps(lib, c["X"], c["C"], 8, sklearn=c.get("sklearn", False))
     assert empties > 0
 
 
@@ -260,8 +265,10 @@ def test_relocation_sequences(lib, name):
 def test_step_sequences(lib, name):
     c = case(name)
     say(f"[gpu] accuracy suite {name}: {c['X'].shape}, k = {len(c['C'])}")
-    _steps(lib, c["X"], c["C"], c["steps"], slice_rows=c.get("slice_rows"), inject=c.get("inject"),
-           sample=c.get("sample"), full_at=c.get("full_at"))
+    _, on_bounds = _steps(lib, c["X"], c["C"], c["steps"], slice_rows=c.get("slice_rows"), inject=c.get("inject"),
+                          sample=c.get("sample"), full_at=c.get("full_at"))
+    say(f"[gpu]   Lloyd steps on the bounds: {on_bounds} of {c['steps']}")
+    assert on_bounds >= c["steps"] // 3      # engaged, as accuracy.py:209 asks
 
 
 def test_centres_past_float16(lib):
@@ -271,15 +278,20 @@ def test_centres_past_float16(lib):
     X, C = c["X"], c["C"]
     ctx = lib.Context()
     ctx.set_parts([X])
+    ctx.bounds(0.5)                      # the decision under test is the bounds', not the gate's (accuracy.py:230)
     for _ in range(5):
         C, _, _ = ctx.lloyd_step(C)
     C2 = C.copy()
     C2[0, 0] = 1e5
     C2[0, 1] = 7e4
+    before = ctx.bounds_info()["on_bounds"]
     for path in ("auto", "mfma", "rows"):
         say(f"[gpu] accuracy suite centres past float16, path {path}")
         tot, labels, best = ctx.run_pass(C2, path=lib.PATHS[path], labels=True, best=True)
         _check_labels(X, C2, labels, best)
         if path == "auto":
             _check_suite_bar(X, C2, labels, tot)
+            info = ctx.bounds_info()
+            say(f"[gpu]   bounds: {info}")
+            assert info["on_bounds"] > before, "the pass with the planted centre should run on the bounds"
     ctx.close()
