@@ -34,6 +34,7 @@ DESCRIPTIONS = {
     "pixels_d4": "96M x 4 fp32, k=12, 12-class clipped correlated mixture",
     "embed_d768": "1M x 768 fp32, k=1024, unit-norm vMF-style embeddings",
     "embed_d1536": "1M x 1536 fp32, k=1024, unit-norm vMF-style embeddings",
+    "blobs_d960": "1M x 960 fp32, k=1024, GIST-width 1024-blob mixture, k-means++ start",
 }
 
 
@@ -143,6 +144,8 @@ def main():
                          "take some tens of milliseconds of work to settle)")
     ap.add_argument("--workload", default="outliers_d32", choices=sorted(DESCRIPTIONS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-bounds", action="store_true",
+                    help="turn the per-centre bounds between passes off (every wide-row pass screens every pair)")
     ap.add_argument("--approx", action="store_true",
                     help="exact=False: the wide-row screen's minimiser taken on trust (other shapes run exact)")
     ap.add_argument("--seed-probe", action="store_true",
@@ -184,6 +187,8 @@ def main():
     n, d = X.shape
     ctx = _lib.Context(0)
     ctx.set_parts([X])
+    if a.no_bounds:
+        ctx.bounds(0.0)
     log(f"[bench] data on device: {n} x {d}, k={k}")
 
     # warmup, then exactly `steps` Lloyd iterations timed by the host clock around device synchronisations.
@@ -209,17 +214,21 @@ def main():
 
     # dominant kernel: HIP events around every launch on the engine's stream, over the same loop
     ctx.profile(True)
+    b0 = ctx.bounds_info()
     ctx.fit(C0, a.steps, -1.0, mode=mode)
     prof = ctx.profile_read()
     pass_ms = ctx.profile_passes()
     ctx.profile(False)
+    b1 = ctx.bounds_info()
+    bounds = {"passes_on_bounds": b1["on_bounds"] - b0["on_bounds"], "builds": b1["builds"] - b0["builds"],
+              "tracked": b1["tracked"] - b0["tracked"], "last_fraction": b1["last_fraction"]}
     log("[bench] per-pass ms (events): " + " ".join(f"{t:.4f}" for t in pass_ms))
     stream_gbs = ctx.stream_probe(1 << 30, 10)
     log(f"[bench] streaming read probe: {stream_gbs:.1f} GB/s")
     kname, (kms, kcount) = max(prof.items(), key=lambda kv: kv[1][0])
     avg_ms = kms / kcount
     log("[bench] kernels: " + ", ".join(f"{k_}: {v[0] / v[1] * 1e3:.1f} us x{v[1]}" for k_, v in prof.items()))
-    if a.workload.startswith("embed_d"):
+    if a.workload.startswith("embed_d") or a.workload == "blobs_d960":
         flops = 2.0 * n * k * d
         achieved = flops / (avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -258,6 +267,7 @@ def main():
                                    "a fit accumulates every row, later passes only the rows whose label changed "
                                    "(on the wide-row path, when at most half the rows changed)"},
         "stream_read_gbs": round(stream_gbs, 1),
+        "bounds": bounds,
         "final_inertia": inertia,
         "roofline": roof,
         "cpu_baseline": cpu,

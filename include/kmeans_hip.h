@@ -124,7 +124,7 @@ int32_t km_pass_noalloc(km_ctx *ctx, const float *X, int64_t rows, int32_t dims,
 /* Per-centre lower bounds between Lloyd passes (the reference's Elkan bounds, core.py:1690-2015). Exact passes on the
  * wide-row path from 256 dims and 64 centres keep, per (row, centre), a float16 lower bound on the distance and per
  * row an upper bound, and run a pass on them (exact scoring of only the centres a bound cannot rule out; the same
- * labels and best, bit for bit) when a strided sample of 8192 rows says at most max_visited of the (row, centre)
+ * labels and best, bit for bit) when a strided sample of 2048 rows says at most max_visited of the (row, centre)
  * pairs need scoring - the reference's gate BOUNDS_MAX_VISITED (core.py:516, 2063-2106). km_bounds sets that
  * fraction for ctx (default 0.05; 0 turns the bounds off and frees nothing until the data changes).
  * km_bounds_info reports, since the data was set: passes tracked, passes run on the bounds, passes that wrote

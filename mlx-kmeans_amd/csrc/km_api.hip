@@ -117,7 +117,8 @@ struct km_ctx {
     DBuf<float> bnd_ub, bnd_S, bnd_delta, bnd_Clast;
     DBuf<uint32_t> bnd_ubl;
     DBuf<km_bnd> bnd_st;
-    std::vector<int64_t> bnd_off;
+    DBuf<float> bnd_raw;            // the sample tiles' raw screen values (a screened pass's resample reads them)
+    std::vector<int64_t> bnd_off, bnd_soff;   // per slice: its first bound, its first sample tile
     bool bnd_valid = false;         // the device state describes this data and bnd_k
     int bnd_k = 0;
     double bnd_max_visited = 0.05;  // the reference's BOUNDS_MAX_VISITED (core.py:516); 0 turns the bounds off
@@ -285,6 +286,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->bnd_Clast.release();
     c->bnd_ubl.release();
     c->bnd_st.release();
+    c->bnd_raw.release();
     c->wd_bcnt.release();
     c->wd_e.release();
     c->wd_H.release();
@@ -459,10 +461,9 @@ static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags
 
 // Per-centre bounds for this wide-row pass: offered to exact passes from KM_BND_MIN_DIMS dims and KM_BND_MIN_K
 // centres with packed keys, within KM_BND_MAX_BYTES of float16 bounds (the reference's _bounds_ok, core.py:1722-1724),
-// unless turned off. Sizes the state (a new data set or k starts it again) and queues the drift, the sample count and
-// the decision; returns whether the pass is tracked, with the sample stride.
-static int prepare_bounds(km_ctx *c, int k, int mode, const km_big_plan &bp0, const float *Cin, const int32_t *stop,
-                          bool *use, int64_t *tstride) {
+// unless turned off. Sizes the state (a new data set or k starts it again) and returns whether the pass is tracked,
+// with the sample stride.
+static int prepare_bounds(km_ctx *c, int k, int mode, const km_big_plan &bp0, bool *use, int64_t *tstride) {
     *use = false;
     if (c->bnd_max_visited <= 0.0 || mode != KM_EXACT || c->d < KM_BND_MIN_DIMS || k < KM_BND_MIN_K || bp0.ib <= 0)
         return KM_OK;
@@ -489,19 +490,32 @@ static int prepare_bounds(km_ctx *c, int k, int mode, const km_big_plan &bp0, co
         c->bnd_k = k;
     }
     *tstride = std::max<int64_t>(1, tiles / KM_BND_SAMPLE_TILES);
+    c->bnd_soff.clear();
+    int64_t stiles = 0;
+    for (auto &p : c->parts) {
+        c->bnd_soff.push_back(stiles);
+        stiles += ((p.rows + 31) / 32 + *tstride - 1) / *tstride;
+    }
+    HIPCHK(c, c->bnd_raw.ensure((size_t)stiles * bp0.nchunks * 1024));
+    *use = true;
+    return KM_OK;
+}
+
+// A tracked pass: each centre's drift, the sample tiles' count, and the decision (every gate of the pass is on the
+// device).
+static int queue_bounds_gate(km_ctx *c, int k, const float *Cin, int64_t tstride, int nchunks, const int32_t *stop) {
     km_bnd *bs = c->bnd_st.p;
-    const float hi = km_bnd_hi(c->d);
     HIPCHK(c, launch(c, KK_BOUNDS, [&] {
         return km_launch_bnd_drift(Cin, c->bnd_Clast.p, k, c->d, c->bnd_valid ? 1 : 0, c->bnd_S.p, c->bnd_delta.p, bs,
                                    stop, c->stream);
     }));
+    const float hi = km_bnd_hi(c->d);
     int64_t row0 = 0;
     for (size_t i = 0; i < c->parts.size(); i++) {
         const Part &p = c->parts[i];
-        HIPCHK(c, launch(c, KK_BOUNDS, [&] {
-            return km_launch_bnd_count(c->bnd_lb.p + c->bnd_off[i], c->bnd_ub.p + row0, c->bnd_ubl.p + row0, p.rows, k,
-                                       bp0.nchunks, *tstride, c->bnd_S.p, c->bnd_delta.p, hi, bs, stop, c->dev.cus,
-                                       c->stream);
+        HIPCHK(c, launch(c, KK_BOUNDS_SAMPLE, [&] {
+            return km_launch_bnd_count(c->bnd_lb.p + c->bnd_off[i], c->bnd_ub.p + row0, c->bnd_ubl.p + row0, p.rows,
+                                       k, nchunks, tstride, c->bnd_S.p, c->bnd_delta.p, hi, bs, stop, c->stream);
         }));
         row0 += p.rows;
     }
@@ -509,7 +523,6 @@ static int prepare_bounds(km_ctx *c, int k, int mode, const km_big_plan &bp0, co
         return km_launch_bnd_decide(bs, c->bnd_max_visited, c->bnd_S.p, k, stop, c->stream);
     }));
     c->bnd_valid = true;
-    *use = true;
     return KM_OK;
 }
 
@@ -578,13 +591,17 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     bool bnd = false;
     int64_t tstride = 1;
     {
-        const int r = prepare_bounds(c, k, mode, bp0, Cin, stop, &bnd, &tstride);
+        const int r = prepare_bounds(c, k, mode, bp0, &bnd, &tstride);
         if (r) return r;
     }
     km_bnd *bs = bnd ? c->bnd_st.p : nullptr;
     HIPCHK(c, launch(c, KK_BIG_PREP, [&] {
         return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop, c->stream);
     }));
+    if (bnd) {
+        const int r = queue_bounds_gate(c, k, Cin, tstride, bp0.nchunks, stop);
+        if (r) return r;
+    }
     int64_t row0 = 0;
     for (size_t i = 0; i < c->parts.size(); i++) {
         const Part &p = c->parts[i];
@@ -594,24 +611,29 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
                 return km_launch_big_centres(bp0, Cin, k, d, c->bcsq.p, c->bcn.p, c->cop.p, c->bmax.p, c->ctl, stop,
                                              c->stream);
             }));
-        // a tracked pass: the plain screen, the bound-writing screen and the bounds list are all queued, and the
-        // decision on the device lets the ones this pass needs run
+        // a tracked pass: the plain screen, the building screen and the bounds list are all queued, and the
+        // decision on the device lets the one this pass needs run
+        float *sraw = bnd ? c->bnd_raw.p + c->bnd_soff[i] * bp.nchunks * 1024 : nullptr;
         HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
             return km_launch_big_screen(bp, mode, p.x16, p.xsq, c->xmax.p, p.rows, d, c->cop.p, c->bmax.p, k,
                                         c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl,
-                                        bnd ? &bs->skip_plain : stop, c->stream);
+                                        bnd ? &bs->skip_plain : stop, c->stream, sraw, tstride);
         }));
         km_bnd_refresh bref{};
         if (bnd) {
             uint16_t *lb = c->bnd_lb.p + c->bnd_off[i];
             bref = km_bnd_refresh{lb, c->bnd_ub.p + row0, c->bnd_ubl.p + row0, c->bnd_S.p, bp.nchunks,
                                   km_bnd_lo(d) * (1.0f - 0x1p-21f), km_bnd_hi(d) * (1.0f + 0x1p-21f), bs};
-            HIPCHK(c, launch(c, KK_BIG_SCREEN, [&] {
-                return km_launch_big_screen_bnd(bp, p.x16, p.xsq, p.rows, d, c->cop.p, c->bmax.p, k, c->ncand.p,
-                                                c->cand.p, c->over.p, c->multi.p, c->ctl, lb, bref.ub, bref.ubl,
-                                                tstride, bs, c->dev.cus, c->stream);
+            HIPCHK(c, launch(c, KK_BOUNDS_SAMPLE, [&] {
+                return km_launch_bnd_resample(sraw, p.xsq, p.rows, d, bp.DS, c->bmax.p, k, bp.nchunks, tstride, lb,
+                                              bref.ub, bref.ubl, c->bnd_S.p, bs, c->stream);
             }));
-            HIPCHK(c, launch(c, KK_BOUNDS, [&] {
+            HIPCHK(c, launch(c, KK_BIG_SCREEN_BND, [&] {
+                return km_launch_big_screen_bnd(bp, p.x16, p.xsq, p.rows, d, c->cop.p, c->bmax.p, k, c->ncand.p,
+                                                c->cand.p, c->over.p, c->multi.p, c->ctl, lb, bref.ub, bref.ubl, bs,
+                                                c->dev.cus, c->stream);
+            }));
+            HIPCHK(c, launch(c, KK_BOUNDS_LIST, [&] {
                 return km_launch_bnd_list(lb, bref.ub, bref.ubl, p.rows, k, bp.nchunks, c->bnd_S.p, c->bnd_delta.p,
                                           km_bnd_hi(d), c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl, bs,
                                           c->dev.cus, c->stream);

@@ -254,6 +254,23 @@ __global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C
 // window, and at the end keeps the listed centres inside the final window - exactly the centres the final window
 // admits. A half-row with more than KB_HALF of them at once (or non-finite data) sends the row to a full scan.
 
+// The window's error bound E for a row (see above) with DS K-steps, from its |x|^2 (rounded up), |bf16(x) - x| and
+// the centres' maxes {max |c|, max |c|^2, max |f|}; nx gets |x| rounded up.
+template <int DS>
+__device__ __forceinline__ float kb_screen_E(float xsq_up, float exn, const float *__restrict__ maxes, float &nx) {
+    constexpr km_screen_k q = km_screen_consts(16 * DS + 2);
+    return km_screen_E(xsq_up, exn, maxes[0], maxes[1], maxes[2], q, nx);
+}
+
+// The per-centre bounds from screen values: D_c >= |x|^2 + a'_c - E. With |x|^2 >= xsq_up (1 - 2^-18) and every
+// |a'_c| at most max|c|^2 + 2 |x| max|c| + E, the slack 2^-21 (|x|^2 + E + max |a'|) covers the float32 additions,
+// so lbase + a'_c (as computed) is at most D_c.
+__device__ __forceinline__ float kb_lbase(float xsq_up, float E, float nx, const float *__restrict__ maxes) {
+    const float xlo = xsq_up * (1.0f - 0x1p-18f);
+    const float amax = maxes[1] + 2.0f * nx * maxes[0] + E;
+    return (xlo - E) - 0x1p-21f * (xlo + E + amax);
+}
+
 // The wave's 32 rows stay in registers as B operands (4 per K-step): up to 48 K-steps two blocks share a CU (256
 // registers a wave); above that one block does, and the 512 registers of a lone wave per SIMD (accumulation
 // registers included, which the matrix cores read operands from) hold up to 96 K-steps without spilling.
@@ -266,6 +283,8 @@ struct kb_bnd_out {
     uint32_t *ubl;
     float lo, hi;
     bool lists;   // also the candidate lists (a tile the plain screen does not take this pass)
+    float *sraw;        // plain instance: the sample tiles' raw screen values (null: none)
+    int64_t sstride;    // ... of the tiles t with t % sstride == 0
 };
 
 // One 32-row tile per wave (tile >= ntiles: a wave of zero rows that only takes part in the block's barriers).
@@ -275,10 +294,7 @@ __device__ __forceinline__ void kb_screen_tile(
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
     int approx, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
     uint32_t *__restrict__ multi, km_control *__restrict__ ctl, const kb_bnd_out &bnd) {
-    constexpr int DP = 16 * DS, AK = DS + 1, NACC = DP + 2;
-    constexpr float GACC = (float)(2.04 * kb_gamma(NACC) * (1.0 + 0x1p-20));
-    constexpr float GAM2 = (float)((1.01 * kb_gamma(NACC) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20));
-    constexpr float FLUSH = (float)0x1p-119;
+    constexpr int DP = 16 * DS, AK = DS + 1;
     constexpr float TINY = (float)((DP + 2) * 0x1p-118);
     extern __shared__ float lds[];
     char *ring = reinterpret_cast<char *>(lds);   // two slices of at most kb_slice(DS) K-steps, 1 KB each
@@ -369,20 +385,10 @@ __device__ __forceinline__ void kb_screen_tile(
     const float exn = real_row ? xsq[2 * row + 1] : 0.0f;
     // per-row window terms: T(m) = a + margin(a), a = m + rho |m|, for the row's smallest key m so far. T only
     // falls as m falls, so a centre kept against an earlier T is a superset of those the final T admits.
-    const float cnmax = maxes[0], csqmax = maxes[1], fmax = maxes[2];
     const float GDIR = (float)(kb_gamma(d + 2) / (1.0 - kb_gamma(d + 2)) * (1.0 + 0x1p-20));
-    const float nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
-    const float E = (2.0f * exn * cnmax + nx * fmax + exn * fmax) * (1.0f + 0x1p-20f) + GACC * nx * cnmax +
-                    GAM2 * csqmax + FLUSH * (nx + cnmax) + TINY;
-    // Bound-writing instance: D_c >= |x|^2 + a'_c - E. With |x|^2 >= xsq_up (1 - 2^-18) and every |a'_c| at most
-    // max|c|^2 + 2 |x| max|c| + E, the slack 2^-21 (|x|^2 + E + max |a'|) covers the float32 additions, so
-    // lbase + a'_c (as computed) is at most D_c.
-    float lbase = 0.0f;
-    if (BND) {
-        const float xlo = xsq_up * (1.0f - 0x1p-18f);
-        const float amax = csqmax + 2.0f * nx * cnmax + E;
-        lbase = (xlo - E) - 0x1p-21f * (xlo + E + amax);
-    }
+    float nx;
+    const float E = kb_screen_E<DS>(xsq_up, exn, maxes, nx);
+    const float lbase = BND ? kb_lbase(xsq_up, E, nx, maxes) : 0.0f;   // the bound-writing instance's
     // a key bound Tp with key <= Tp whenever key - rho |key| <= T
     auto key_bound = [&](float m) {
         const float akm = m + rho * fabsf(m);
@@ -402,6 +408,10 @@ __device__ __forceinline__ void kb_screen_tile(
     uint16_t *lidx = reinterpret_cast<uint16_t *>(reinterpret_cast<float *>(ring + 2 * SLK * 1024) +
                                                   (size_t)KB_WAVES * KB_HALF * 64) +
                      (size_t)wave * KB_HALF * 64 + lane;
+    // a sample tile of the per-centre bounds (32-bit arithmetic: a slice has fewer than 2^27 tiles)
+    const bool sample = !BND && bnd.sraw && have && (uint32_t)tile % (uint32_t)bnd.sstride == 0u;
+    float *sdst = sample ? bnd.sraw + ((int64_t)((uint32_t)tile / (uint32_t)bnd.sstride) * nchunks * 64 + lane) * 16
+                         : nullptr;
     issue(0);
     float m1 = 3.4e38f;
     int cnt = 0;
@@ -418,6 +428,13 @@ __device__ __forceinline__ void kb_screen_tile(
             // read it must be compiled code, whose hazard tracking inserts the wait states an MFMA result needs
             // (inline assembly here read stale accumulators)
             m1 = PACK ? kb_min(m1, key[v]) : fminf(m1, key[v]);
+        }
+        if (!BND && sample) {   // a sample tile: its raw values, 64 B per lane
+            float4 *dst = reinterpret_cast<float4 *>(sdst + (int64_t)ch * 1024);
+            dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+            dst[2] = make_float4(acc[8], acc[9], acc[10], acc[11]);
+            dst[3] = make_float4(acc[12], acc[13], acc[14], acc[15]);
         }
         if (BND && have) {   // this chunk's lower bounds, 32 contiguous bytes per lane
             uint32_t pk[8];
@@ -525,40 +542,38 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen(
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
     int approx, const uint32_t *__restrict__ xmax, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand,
     uint32_t *__restrict__ over, uint32_t *__restrict__ multi, km_control *__restrict__ ctl,
-    const int32_t *__restrict__ stop) {
+    const int32_t *__restrict__ stop, float *__restrict__ sraw, int64_t sstride) {
     if (stop && *stop) return;
     // Approximate mode only while this pass's centres pass the reference's half-precision guard (core.py:1055-1058):
     // sqrt(max |x|^2 max |c|^2) < 65504 / 4, from the data's largest |x|^2 (rounded up, +inf if any row is not
     // finite) and the largest |c|^2 of the centres. Otherwise the pass is exact.
     if (approx) approx = sqrt((double)kb_f32(*xmax) * (double)maxes[1]) < KB_APPROX_LIMIT;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kb_bnd_out out{};
+    out.sraw = sraw;
+    out.sstride = sstride;
     kb_screen_tile<DS, PACK, false>((int64_t)blockIdx.x * KB_WAVES + wave, X16T, xsq, n, d, Cop, maxes, k, nchunks,
-                                    ib, rho, approx, ncand, cand, over, multi, ctl, kb_bnd_out{});
+                                    ib, rho, approx, ncand, cand, over, multi, ctl, out);
 }
 
-// The bound-writing screen of a tracked exact pass (packed keys): the sample tiles (t % tstride == 0), bounds only
-// (the plain screen lists their candidates), or every tile, bounds and lists, when the pass builds (the plain screen
-// then stands down); a grid of blocks loops over them (a pass that writes only the sample keeps most blocks idle, at
-// no more cost than their launch).
+// The screen of a pass that builds the per-centre bounds (packed keys): every tile's lists, as the plain screen
+// writes them, plus its float16 bounds and every row's ub. A grid of one round of blocks loops over the tiles (on
+// the passes that do not build, the launch costs only its blocks' start).
 template <int DS>
 __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen_bnd(
     const uint16_t *__restrict__ X16T, const float *__restrict__ xsq, int64_t n, int d,
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
     uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
     uint32_t *__restrict__ multi, km_control *__restrict__ ctl, uint16_t *__restrict__ lb, float *__restrict__ ub,
-    uint32_t *__restrict__ ubl, float lo, float hi, int64_t tstride, const km_bnd *__restrict__ bs) {
+    uint32_t *__restrict__ ubl, float lo, float hi, const km_bnd *__restrict__ bs) {
     if (bs->skip_bscreen) return;
-    const bool all = bs->build != 0;
     const int64_t ntiles = (n + 31) / 32;
-    const int64_t step = all ? 1 : tstride;
-    const int64_t nwork = (ntiles + step - 1) / step;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const kb_bnd_out out{lb, ub, ubl, lo, hi, all};
-    for (int64_t wb = blockIdx.x; wb * KB_WAVES < nwork; wb += gridDim.x) {   // block-uniform
+    const kb_bnd_out out{lb, ub, ubl, lo, hi, true, nullptr, 1};
+    for (int64_t wb = blockIdx.x; wb * KB_WAVES < ntiles; wb += gridDim.x) {   // block-uniform
         __syncthreads();   // every wave is done with the previous tile's A slices before the ring is refilled
-        const int64_t w = wb * KB_WAVES + wave;
-        kb_screen_tile<DS, true, true>(w < nwork ? w * step : ntiles, X16T, xsq, n, d, Cop, maxes, k, nchunks, ib,
-                                       rho, 0, ncand, cand, over, multi, ctl, out);
+        kb_screen_tile<DS, true, true>(wb * KB_WAVES + wave, X16T, xsq, n, d, Cop, maxes, k, nchunks, ib, rho, 0,
+                                       ncand, cand, over, multi, ctl, out);
     }
 }
 
@@ -1102,7 +1117,7 @@ __global__ __launch_bounds__(256) void k_big_scatter_g(const uint32_t *__restric
 
 typedef void (*screen_fn)(const uint16_t *, const float *, int64_t, int, const uint16_t *, const float *, int, int,
                           int, float, int, const uint32_t *, uint16_t *, uint16_t *, uint32_t *, uint32_t *,
-                          km_control *, const int32_t *);
+                          km_control *, const int32_t *, float *, int64_t);
 
 template <bool PACK>
 static screen_fn kb_screen_for(int DS) {
@@ -1180,8 +1195,9 @@ hipError_t km_launch_big_centres(const km_big_plan &pl, const float *C, int k, i
 hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq,
                                 const uint32_t *xmax, int64_t n, int d, const uint16_t *Cop, const float *maxes, int k,
                                 uint16_t *ncand, uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
-                                const int32_t *stop, hipStream_t s) {
+                                const int32_t *stop, hipStream_t s, float *sraw, int64_t sstride) {
     const bool pack = pl.ib > 0;
+    if (sraw && (!pack || sstride < 1)) return hipErrorInvalidValue;
     screen_fn fn = pack ? kb_screen_for<true>(pl.DS) : kb_screen_for<false>(pl.DS);
     if (!fn) return hipErrorInvalidValue;
     const float rho = pack ? (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23) : 0.0f;
@@ -1197,7 +1213,7 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
     }
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * KB_WAVES), lds, s, X16T,
                        xsq, n, d, Cop, maxes, k, pl.nchunks, pl.ib, rho, approx, xmax, ncand, cand, over, multi, ctl,
-                       stop);
+                       stop, sraw, sstride);
     return hipGetLastError();
 }
 
@@ -1245,8 +1261,7 @@ template <int DS>
 static hipError_t kb_launch_screen_bnd(const km_big_plan &pl, const uint16_t *X16T, const float *xsq, int64_t n, int d,
                                        const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand,
                                        uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
-                                       uint16_t *lb, float *ub, uint32_t *ubl, int64_t tstride, km_bnd *bs, int cus,
-                                       hipStream_t s) {
+                                       uint16_t *lb, float *ub, uint32_t *ubl, km_bnd *bs, int cus, hipStream_t s) {
     const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
     const int ak = DS + 1, spc = (ak + kb_slice(DS) - 1) / kb_slice(DS), slk = (ak + spc - 1) / spc;
     const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * KB_HALF * 64 * 4;
@@ -1260,23 +1275,23 @@ static hipError_t kb_launch_screen_bnd(const km_big_plan &pl, const uint16_t *X1
     const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)cus * (DS > 48 ? 1 : 2)));
     hipLaunchKernelGGL(k_big_screen_bnd<DS>, dim3((unsigned)blocks), dim3(64 * KB_WAVES), lds, s, X16T, xsq, n, d,
                        Cop, maxes, k, pl.nchunks, pl.ib, rho, ncand, cand, over, multi, ctl, lb, ub, ubl,
-                       km_bnd_lo(d) * (1.0f - 0x1p-21f), km_bnd_hi(d) * (1.0f + 0x1p-21f), tstride, bs);
+                       km_bnd_lo(d) * (1.0f - 0x1p-21f), km_bnd_hi(d) * (1.0f + 0x1p-21f), bs);
     return hipGetLastError();
 }
 
 hipError_t km_launch_big_screen_bnd(const km_big_plan &pl, const uint16_t *X16T, const float *xsq, int64_t n, int d,
                                     const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
                                     uint32_t *over, uint32_t *multi, km_control *ctl, uint16_t *lb, float *ub,
-                                    uint32_t *ubl, int64_t tstride, km_bnd *bs, int cus, hipStream_t s) {
+                                    uint32_t *ubl, km_bnd *bs, int cus, hipStream_t s) {
     if (pl.ib <= 0) return hipErrorInvalidValue;   // packed keys only (k <= KM_BIG_PACK_MAX_K)
     switch (pl.DS) {
-        case 16: return kb_launch_screen_bnd<16>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
-        case 24: return kb_launch_screen_bnd<24>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
-        case 32: return kb_launch_screen_bnd<32>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
-        case 48: return kb_launch_screen_bnd<48>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
-        case 60: return kb_launch_screen_bnd<60>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
-        case 64: return kb_launch_screen_bnd<64>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
-        case 96: return kb_launch_screen_bnd<96>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, tstride, bs, cus, s);
+        case 16: return kb_launch_screen_bnd<16>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
+        case 24: return kb_launch_screen_bnd<24>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
+        case 32: return kb_launch_screen_bnd<32>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
+        case 48: return kb_launch_screen_bnd<48>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
+        case 60: return kb_launch_screen_bnd<60>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
+        case 64: return kb_launch_screen_bnd<64>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
+        case 96: return kb_launch_screen_bnd<96>(pl, X16T, xsq, n, d, Cop, maxes, k, ncand, cand, over, multi, ctl, lb, ub, ubl, bs, cus, s);
         default: return hipErrorInvalidValue;
     }
 }

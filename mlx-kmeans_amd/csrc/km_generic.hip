@@ -20,7 +20,7 @@ const char *const km_kernel_names[KK_COUNT] = {
     "km_assign_rows", "km_accum_generic", "km_reduce",     "km_finish",    "km_normalise",
     "km_fused_lowd",  "km_fused_mfma",    "km_big_prep",   "km_big_screen", "km_big_rescore",
     "km_big_accum",   "km_seed_pp",       "km_relocate",
-    "km_change_sums", "km_bounds"};
+    "km_change_sums", "km_bounds",      "km_bounds_list", "km_big_screen_bnd", "km_bounds_sample"};
 
 // Neumaier's compensated add, the reference's KAHAN_ADD (core.py:244-247): t = s + v; the rounding error of
 // that add goes to c; the true running sum is s + c.

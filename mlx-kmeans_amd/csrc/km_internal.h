@@ -69,7 +69,10 @@ enum km_kernel_id {
     KK_SEED_PP,
     KK_RELOCATE,
     KK_CHANGE,   // the wide-row fit loop's change count, gate and change-only sums
-    KK_BOUNDS,   // the per-centre bounds: drift, sample count, decision, candidate lists
+    KK_BOUNDS,   // the per-centre bounds: drift, sample count, decision
+    KK_BOUNDS_LIST,   // the per-centre bounds: a pass's candidate lists
+    KK_BIG_SCREEN_BND,   // the screen of a pass that builds the per-centre bounds
+    KK_BOUNDS_SAMPLE,    // the per-centre bounds' sample tiles: count and fresh bounds
     KK_COUNT
 };
 extern const char *const km_kernel_names[KK_COUNT];
@@ -236,10 +239,12 @@ hipError_t km_launch_relocate(const double *tot, int k, int d, int64_t n, const 
 #define KM_RELOC_NEMPTY_WORD 5
 // KM_APPROX approximates from KM_APPROX_MIN_DIMS dims while sqrt(max |x|^2 max |c|^2) < 65504 / 4; exact otherwise
 #define KM_APPROX_MIN_DIMS 64
+// sraw (may be null): the raw screen values a' of the tiles t with t % sstride == 0 (packed keys only),
+// sraw[((t / sstride) nchunks + ch) 64 + lane][16], for the per-centre bounds' sample
 hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t *X16T, const float *xsq,
                                 const uint32_t *xmax, int64_t n, int d, const uint16_t *Cop, const float *maxes, int k,
                                 uint16_t *ncand, uint16_t *cand, uint32_t *over, uint32_t *multi, km_control *ctl,
-                                const int32_t *stop, hipStream_t s);
+                                const int32_t *stop, hipStream_t s, float *sraw = nullptr, int64_t sstride = 1);
 // lite: the pass returns no per-row distances; single-candidate rows take their label without one. okeys: n words
 // for the full scan of the overflow rows split over centre ranges (above 256 centres; null: one range)
 // The rows loop for all n rows of a part, tiled (64 rows x 64 centres per block step, 32 dims at a time through
@@ -267,7 +272,10 @@ hipError_t km_launch_big_accum(const km_big_plan &pl, const float *X, int64_t n,
 #define KM_BND_MIN_DIMS 256          // the reference's BOUNDS_MIN_DIMS (core.py:513)
 #define KM_BND_MIN_K 64              // the reference's TILES_MIN_K, which _bounds_ok requires (core.py:1722-1724)
 #define KM_BND_MAX_BYTES ((size_t)16 << 30)   // the reference's BOUNDS_MAX_BYTES (core.py:515)
-#define KM_BND_SAMPLE_TILES 256      // 32-row tiles the gate samples: the reference's BOUNDS_SAMPLE_ROWS (8192)
+#define KM_BND_SAMPLE_TILES 64       // 32-row tiles the gate samples (2048 rows; the reference's BOUNDS_SAMPLE_ROWS is
+                                     // 8192): each sampled tile re-reads every centre operand, so the sample's cost is
+                                     // in proportion to its tiles, and 2048 rows x k centres estimate a fraction near
+                                     // 5 % to well under a percent
 __host__ __device__ inline int64_t km_bnd_index(int64_t row, int c, int nchunks) {
     const int ch = c >> 5, cc = c & 31;
     const int h = (cc >> 2) & 1, v = ((cc >> 3) << 2) | (cc & 3);
@@ -276,12 +284,33 @@ __host__ __device__ inline int64_t km_bnd_index(int64_t row, int c, int nchunks)
 // centre held at value v of half h of chunk ch (the screen's accumulator order)
 __host__ __device__ inline int km_bnd_centre(int ch, int h, int v) { return 32 * ch + 8 * (v >> 2) + 4 * h + (v & 3); }
 
+// The wide-row screen's error bound (km_big.hip explains it): |a'_c - A_c| <= E for every centre, from the row's |x|^2
+// (rounded up) and |bf16(x) - x|, the centres' max |c|, max |c|^2 and max |bf16(-2c) + 2c|, and the constants of
+// nacc = 16 DS + 2 accumulated terms (km_screen_consts); nx gets |x| rounded up.
+__host__ __device__ constexpr double km_screen_gamma(int m) {
+    return m * 5.9604644775390625e-08 / (1.0 - m * 5.9604644775390625e-08);
+}
+struct km_screen_k {
+    float gacc, gam2, tiny;
+};
+__host__ __device__ constexpr km_screen_k km_screen_consts(int nacc) {
+    return km_screen_k{(float)(2.04 * km_screen_gamma(nacc) * (1.0 + 0x1p-20)),
+                       (float)((1.01 * km_screen_gamma(nacc) + 0x1p-16 + 0x1p-23) * (1.0 + 0x1p-20)),
+                       (float)(nacc * 0x1p-118)};
+}
+__host__ __device__ inline float km_screen_E(float xsq_up, float exn, float cnmax, float csqmax, float fmax,
+                                             km_screen_k q, float &nx) {
+    nx = __builtin_sqrtf(xsq_up) * (1.0f + 0x1p-22f);
+    return (2.0f * exn * cnmax + nx * fmax + exn * fmax) * (1.0f + 0x1p-20f) + q.gacc * nx * cnmax + q.gam2 * csqmax +
+           (float)0x1p-119 * (nx + cnmax) + q.tiny;
+}
+
 struct km_bnd {
     int32_t skip_plain;    // nonzero: the plain screen stands down (bounds, a build, or the loop stopped)
     int32_t skip_bscreen;  // nonzero: the bound-writing screen stands down (bounds, or the loop stopped)
     int32_t skip_list;     // nonzero: the bounds list stands down (a screened pass, or the loop stopped)
     int32_t build;         // this pass writes every tile's bounds (else the sample tiles' only)
-    int32_t sample_ok;     // the sample tiles' bounds describe the previous tracked pass
+    int32_t sample_ok;     // the sample tiles have bounds from an earlier tracked pass
     int32_t built;         // every tile's bounds do (refreshes are worth writing)
     unsigned long long visits;     // sampled (row, centre) pairs this pass would visit, the ub centre excluded
     unsigned long long pairs;      // sampled (row, centre) pairs
@@ -297,11 +326,17 @@ float km_bnd_hi(int d);
 // new state: S = 0, nothing sampled, nothing built); Clast = C.
 hipError_t km_launch_bnd_drift(const float *C, float *Clast, int k, int d, int valid, float *S, float *delta,
                                km_bnd *bs, const int32_t *stop, hipStream_t s);
-// The sampled count of one slice (tiles t with t % tstride == 0), then (once) the decision and the gates.
+// Per slice, the sample tiles (t % tstride == 0): the count of the pairs the stored bounds would visit now; then
+// (once) the decision and the gates.
 hipError_t km_launch_bnd_count(const uint16_t *lb, const float *ub, const uint32_t *ubl, int64_t n, int k,
                                int nchunks, int64_t tstride, const float *S, const float *delta, float hi,
-                               km_bnd *bs, const int32_t *stop, int cus, hipStream_t s);
+                               km_bnd *bs, const int32_t *stop, hipStream_t s);
 hipError_t km_launch_bnd_decide(km_bnd *bs, double max_visited, float *S, int k, const int32_t *stop, hipStream_t s);
+// After a plain screen that wrote the sample tiles' raw screen values sraw (km_launch_big_screen with sraw): their
+// bounds in the current frame and their rows' ub / ubl; gated on bs->skip_plain. ds: the screen's K-steps.
+hipError_t km_launch_bnd_resample(const float *sraw, const float *xsq, int64_t n, int d, int ds, const float *maxes,
+                                  int k, int nchunks, int64_t tstride, uint16_t *lb, float *ub, uint32_t *ubl,
+                                  const float *S, km_bnd *bs, hipStream_t s);
 // A pass on the bounds, one slice: candidate lists (ncand/cand/over/multi as the screen writes them) and every
 // row's raised ub; gated on bs->skip_list.
 hipError_t km_launch_bnd_list(const uint16_t *lb, float *ub, const uint32_t *ubl, int64_t n, int k, int nchunks,
@@ -311,13 +346,12 @@ hipError_t km_launch_bnd_list(const uint16_t *lb, float *ub, const uint32_t *ubl
 hipError_t km_launch_bnd_overfix(const uint32_t *over, const km_control *ctl, const uint32_t *labels,
                                  const float *best, float *ub, uint32_t *ubl, float hi, const km_bnd *bs,
                                  const int32_t *stop, hipStream_t s);
-// Bound-writing screen (one slice): the screen with every row's ub / ubl and the float16 bounds of the sample
-// tiles (t % tstride == 0), or of every tile when bs->build; gated on bs->skip_bscreen.
-struct km_big_plan;
+// Bound-writing screen (one slice) of a build: the screen's lists plus every row's ub / ubl and every tile's float16
+// bounds; gated on bs->skip_bscreen.
 hipError_t km_launch_big_screen_bnd(const km_big_plan &pl, const uint16_t *X16T, const float *xsq, int64_t n, int d,
                                     const uint16_t *Cop, const float *maxes, int k, uint16_t *ncand, uint16_t *cand,
                                     uint32_t *over, uint32_t *multi, km_control *ctl, uint16_t *lb, float *ub,
-                                    uint32_t *ubl, int64_t tstride, km_bnd *bs, int cus, hipStream_t s);
+                                    uint32_t *ubl, km_bnd *bs, int cus, hipStream_t s);
 // Refreshes the rescoring and the overflow fix write (null: none): the bounds of a slice, S, lo/hi
 struct km_bnd_refresh {
     uint16_t *lb;        // the slice's bounds

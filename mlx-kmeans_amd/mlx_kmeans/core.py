@@ -26,7 +26,7 @@ PART_MAX_ELEMENTS = 2**32 - 1           # elements per slice: the reference's li
                                         # refused above it as the reference does (core.py:2028-2032)
 
 # Per-centre bounds between passes (core.py:1690-2015): exact wide-row passes from 256 dims and 64 centres keep a
-# lower bound per (row, centre) and run on them while a sample of 8192 rows says at most this fraction of the
+# lower bound per (row, centre) and run on them while a sample of 2048 rows says at most this fraction of the
 # pairs needs scoring (the reference's BOUNDS_MAX_VISITED, core.py:516). Read at every pass; 0 turns them off.
 BOUNDS_MAX_VISITED = 0.05
 

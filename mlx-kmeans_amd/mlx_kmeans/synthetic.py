@@ -12,6 +12,10 @@
     embed_d768     1M x 768, k=1024: unit rows normalize(centre + N(0, 0.15^2 I)) around 1024 random unit
                    centres; start: 1024 seeded rows; 15 iterations
     embed_d1536    the same at 1536 dims (the widest rows the matrix-core screen takes)
+    blobs_d960     1M x 960, k=1024: GIST-like width, 1024-component isotropic mixture, means ~U[-1,1]^960, sigma 1
+                   (the reference's bounds sequence, tests/accuracy.py:305-306, at 1M rows and one blob per
+                   centre); start: greedy k-means++ on a 20,480-row subsample; 20 iterations. Well separated: the
+                   per-centre bounds between passes take over once the fit settles.
 
 Every generator takes n (rows) so tests can draw the same distribution at smaller sizes.
 """
@@ -149,6 +153,19 @@ def embed_d1536(n=1_000_000, seed=0, k=1024):
     return _unit_rows("embed_d1536", n, 1536, seed, k)
 
 
+def blobs_d960(n=1_000_000, seed=0, k=1024):
+    rng = np.random.default_rng(seed)
+    means = rng.uniform(-1.0, 1.0, size=(k, 960)).astype(np.float32)
+    X = np.empty((n, 960), np.float32)
+    step = 250_000
+    for a in range(0, n, step):
+        b = min(n, a + step)
+        lab = rng.integers(0, k, size=b - a)
+        X[a:b] = means[lab] + rng.standard_normal((b - a, 960), dtype=np.float32)
+    C0 = kmeans_pp_init([X], n, k, rng)
+    return dict(name="blobs_d960", X=X, C0=C0, k=k, iters=20)
+
+
 WORKLOADS = {
     "blobs_d32": blobs_d32,
     "lowd_d8": lowd_d8,
@@ -156,4 +173,5 @@ WORKLOADS = {
     "pixels_d4": pixels_d4,
     "embed_d768": embed_d768,
     "embed_d1536": embed_d1536,
+    "blobs_d960": blobs_d960,
 }
