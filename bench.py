@@ -191,6 +191,10 @@ def main():
         ctx.bounds(0.0)
     log(f"[bench] data on device: {n} x {d}, k={k}")
 
+    # the streaming-read rate the roofline is read against, measured first (it also brings the GPU's clocks up
+    # before the warmup passes)
+    stream_gbs = ctx.stream_probe(1 << 30, 10)
+    log(f"[bench] streaming read probe: {stream_gbs:.1f} GB/s")
     # warmup, then exactly `steps` Lloyd iterations timed by the host clock around device synchronisations.
     # tol = -1 never stops the loop, so a workload that reaches a fixed point early still runs every pass.
     mode = _lib.KM_APPROX if a.approx else _lib.KM_EXACT
@@ -223,8 +227,6 @@ def main():
     bounds = {"passes_on_bounds": b1["on_bounds"] - b0["on_bounds"], "builds": b1["builds"] - b0["builds"],
               "tracked": b1["tracked"] - b0["tracked"], "last_fraction": b1["last_fraction"]}
     log("[bench] per-pass ms (events): " + " ".join(f"{t:.4f}" for t in pass_ms))
-    stream_gbs = ctx.stream_probe(1 << 30, 10)
-    log(f"[bench] streaming read probe: {stream_gbs:.1f} GB/s")
     kname, (kms, kcount) = max(prof.items(), key=lambda kv: kv[1][0])
     avg_ms = kms / kcount
     log("[bench] kernels: " + ", ".join(f"{k_}: {v[0] / v[1] * 1e3:.1f} us x{v[1]}" for k_, v in prof.items()))
