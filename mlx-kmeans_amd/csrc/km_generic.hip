@@ -449,12 +449,15 @@ __global__ __launch_bounds__(1024) void k_finish1(const double *__restrict__ tmp
 
 // k_reduce_split whose last block to finish runs the single-block finish: one launch per pass instead of two. Each
 // block writes its range sums (agent-scope stores, written through to the point of coherence) and waits for them
-// to complete; a block barrier orders every thread's stores before thread 0's ticket, an agent-scope
-// acquire-release read-modify-write. The release publishes the block's sums to whichever block later acquires the
-// ticket; the block that takes the last ticket has acquired every earlier block's release (the ticket's
-// modification order is a release sequence), its barrier passes that on to its other threads, and it reads the
-// sums back with agent-scope loads (across XCDs), finishes, and resets the ticket for the next launch (the kernel
-// boundary orders that store before the next launch's tickets).
+// to complete; a block barrier orders every thread's stores before thread 0's ticket, an agent-scope release
+// read-modify-write, which publishes the block's sums. The block that takes the last ticket follows it with an
+// agent-scope acquire fence: its read-modify-write read the value every earlier release's sequence wrote (the
+// ticket's modification order is a release sequence), so the fence synchronises with every block's release. Only
+// that block's thread 0 pays for the acquire (a cache invalidation; one per block, as an acquire-release ticket
+// would have it, measured 1.5-2 us slower per pass). Its barrier passes the result on to its other threads (the
+// caches thread 0 invalidated are the block's); it reads the sums back with agent-scope loads (across XCDs),
+// finishes, and resets the ticket for the next launch (the kernel boundary orders that store before the next
+// launch's tickets).
 __global__ __launch_bounds__(1024) void k_reduce_finish(const float *__restrict__ psum,
                                                         const float *__restrict__ pcomp, int nrb, int64_t kw, int S,
                                                         double *__restrict__ tmp, int k, int d,
@@ -470,12 +473,12 @@ __global__ __launch_bounds__(1024) void k_reduce_finish(const float *__restrict_
     __syncthreads();
     if (threadIdx.x == 0) {
         const unsigned total = gridDim.x * gridDim.y;
-        const unsigned prev = __hip_atomic_fetch_add(&ctl->ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned prev = __hip_atomic_fetch_add(&ctl->ticket, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == total - 1;
+        if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // every block's release, through the ticket
     }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // every thread of the last block, after the barrier
     finish1_body<true>(tmp, S, k, d, tot, Cnext, ctl, pass, tol, flags, Ts);
     if (threadIdx.x == 0) __hip_atomic_store(&ctl->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
