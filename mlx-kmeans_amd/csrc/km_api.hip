@@ -26,6 +26,10 @@ static const int KM_FIT_BATCH = 8;
 // to the previous totals; every KM_REANCHOR_PASSES passes after a recording pass, one pass records every row again,
 // so the totals never carry more than that many passes of change rounding.
 static const int KM_REANCHOR_PASSES = 32;
+// The fused path's change-only passes use the kernel without candidate lists (open rows scanned by the whole
+// wave) while the context's last fit left at most this fraction of rows open: then about 0.1 % of 64-row blocks
+// hold more than four open rows (where the lists start to pay).
+static const double KM_SCAN_ONLY_FRAC = 0.01;
 
 template <class T>
 struct DBuf {
@@ -122,6 +126,8 @@ struct km_ctx {
     bool bnd_valid = false;         // the device state describes this data and bnd_k
     int bnd_k = 0;
     double bnd_max_visited = 0.05;  // the reference's BOUNDS_MAX_VISITED (core.py:516); 0 turns the bounds off
+    double open_frac = -1.0;        // rows the fused screen left open, per row and pass, in this context's last fit
+                                    // on that path (< 0: none yet)
     std::vector<km_slice> wd_slices_h;
     bool wd_ready = false;          // wd_mu and wd_slices describe the current data
     int64_t wd_limit = 0;           // the most changed rows a change-only pass takes
@@ -703,6 +709,8 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         }
         int r = ensure_pass_buffers(c, k, total_rb, false);
         if (r) return r;
+        // where the last fit saw few open rows, its change-only passes take the kernel without candidate lists
+        const int scan_only = lmode == KM_LSTATE_DELTA && c->open_frac >= 0.0 && c->open_frac <= KM_SCAN_ONLY_FRAC;
         int rb = 0;
         int64_t row0 = 0;
         for (size_t i = 0; i < c->parts.size(); i++) {
@@ -712,7 +720,7 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             uint8_t *ls = lmode != KM_LSTATE_NONE ? c->lstate.p + c->lstate_off[i] : nullptr;
             HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
                 return km_launch_mfma(plans[i], want_best, p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p,
-                                      rb, c->ctl, ls, ls, lmode, stop, c->stream);
+                                      rb, c->ctl, ls, ls, lmode, stop, c->stream, scan_only);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;
@@ -730,6 +738,8 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         }
         int r = ensure_pass_buffers(c, k, total_rb, false);
         if (r) return r;
+        // where the last fit saw few open rows, its change-only passes take the kernel without candidate lists
+        const int scan_only = lmode == KM_LSTATE_DELTA && c->open_frac >= 0.0 && c->open_frac <= KM_SCAN_ONLY_FRAC;
         int rb = 0;
         int64_t row0 = 0;
         for (size_t i = 0; i < c->parts.size(); i++) {
@@ -1076,6 +1086,8 @@ extern "C" int32_t km_fit(km_ctx *c, const float *C0, int32_t k, int32_t max_ite
         mark(false);
         if ((r = read_control(c))) return r;
         pass = c->ctl_h->iter;
+        if (c->last_family == FAM_MFMA_FUSED && pass > 0)
+            c->open_frac = (double)c->ctl_h->fallback_rows / ((double)c->n * pass);
         if (c->ctl_h->need_reloc) {
             int ne = 0;
             const int q = c->ctl_h->iter - 1;   // the pass that left clusters empty

@@ -178,9 +178,12 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
 #define KM_LSTATE_NONE 0
 #define KM_LSTATE_RECORD 1
 #define KM_LSTATE_DELTA 2
+// scan_only (KM_LSTATE_DELTA passes): the kernel without the candidate lists for waves with many open rows, every
+// open row scanned by the whole wave (smaller; for data whose open rows are rare).
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
-                          const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s);
+                          const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s,
+                          int scan_only = 0);
 
 // Fused single-read pass for dims <= 16: exact rows loop + deterministic accumulation into per-block partials.
 struct km_lowd_plan {

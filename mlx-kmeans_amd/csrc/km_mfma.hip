@@ -174,6 +174,27 @@ __device__ __forceinline__ void min2_keys(const f32x16 (&a)[Geo<D, KP>::KT], flo
         }
 }
 
+// Candidate bits of this lane's screen values for one tile: bit (8(v/4) + 4h + v%4) of word t is set when
+// a[t][v] <= T2 (the lane's 16 values of centre tile t, for the row its column holds). The values are compared
+// unpacked; T2 = T + 4 RHO |T| + tiny covers the packing perturbation, so the set holds every centre the packed-key
+// window admits. Compiled code, not inline assembly: the values are matrix-core results, and only the compiler's
+// hazard tracking inserts the wait states a vector instruction needs before it may read them.
+template <int D, int KP>
+__device__ __forceinline__ void cand_bits(const f32x16 (&a)[Geo<D, KP>::KT], float T2, int h,
+                                          uint32_t (&w)[Geo<D, KP>::KT]) {
+    using G = Geo<D, KP>;
+#pragma unroll
+    for (int t = 0; t < G::KT; t++) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int v = 15; v >= 0; v--) m = 2u * m + (a[t][v] <= T2 ? 1u : 0u);
+        // byte j of the result = nibble j of the 16-bit mask, then shifted into this half's positions
+        const uint32_t pq = __builtin_amdgcn_perm(m, m, 0x01010000u);   // bytes b0, b0, b1, b1
+        const uint32_t q = ((pq & 0x000f000fu) | ((pq >> 4) & 0x0f000f00u));
+        w[t] = q << (4 * h);
+    }
+}
+
 __device__ __forceinline__ bf16x2 as_bf2(uint32_t v) { return *reinterpret_cast<bf16x2 *>(&v); }
 __device__ __forceinline__ uint32_t bf2_u32(bf16x2 v) { return *reinterpret_cast<uint32_t *>(&v); }
 
@@ -210,6 +231,12 @@ __device__ __forceinline__ void split3(const float (&x)[8], bf16x8 &ph, bf16x8 &
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
+// Open rows (several centres in the window) of a 64-row block up to which the whole wave scores each such row
+// against every centre (one row at a time, lanes over centres); above it each lane rescores its own row against
+// the centres its window lists. The scan costs about 3 D k / 64 + 30 instructions per open row, the lists a
+// second screen, the row exchange and 3 D per listed centre: about four open rows apart.
+static constexpr int KM_SCAN_ROWS = 4;
+
 // Rows reach LDS by direct global->LDS loads (global_load_lds_dwordx4, non-temporal: a pass reads each row once),
 // double-buffered one 64-row block ahead. A block is its 64 rows in order (D floats = NC 16-byte chunks each); one
 // load instruction moves 1 KB, i.e. 64/NC whole rows read contiguously, lane i taking the 16 bytes that land at LDS
@@ -222,13 +249,15 @@ template <int D>
 struct Lay {
     static constexpr int NC = D / 4;           // 16-byte chunks per row
     static constexpr int QI = NC / 2;          // chunks per half row (the screen's reads per tile)
-    static constexpr int RPI = 64 / NC;        // rows per load instruction
     static constexpr int BUF = 64 * D * 4;     // bytes per 64-row block (NC instructions)
+    static constexpr bool SWZ = D == 16 || D == 32 || D == 64;   // rows permuted (NC a power of two)
 };
 
+// 48-dim rows (12 chunks) stay in order: a permutation within 12 chunks cannot keep both read patterns on
+// distinct banks, and the half-row reads' conflicts (rows 192 bytes apart) cost less than the loads they overlap.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-    return D == 16 ? ((r >> 1) & 3) : (r & 7);
+    return !Lay<D>::SWZ ? 0 : D == 16 ? ((r >> 1) & 3) : (r & 7);
 }
 
 // wait until at most N vector memory operations of this wave are outstanding
@@ -242,10 +271,10 @@ template <int D>
 __device__ __forceinline__ void issue_block(const float *__restrict__ X, int64_t r0, int64_t r_end, int lane,
                                             char *buf) {
     using L = Lay<D>;
-    const int p = lane % L::NC;   // this lane's position within its row
 #pragma unroll
     for (int q = 0; q < L::NC; q++) {
-        const int r = q * L::RPI + lane / L::NC;   // block row
+        const int g = q * 64 + lane;           // the 16-byte slot this lane fills
+        const int r = g / L::NC, p = g % L::NC;   // block row, position within the row
         int64_t row = r0 + r;
         row = row < r_end ? row : r_end - 1;
         const float *src = X + row * D + 4 * (p ^ swz<D>(r));
@@ -279,8 +308,9 @@ __device__ __forceinline__ void issue_block_inner_all(const float *blk, uint32_t
 template <int D>
 __device__ __forceinline__ uint32_t issue_voff(int lane, int q) {
     using L = Lay<D>;
-    const int r = q * L::RPI + lane / L::NC;
-    return (uint32_t)((lane / L::NC) * D * 4 + 16 * ((lane % L::NC) ^ swz<D>(r)));
+    if constexpr (!L::SWZ) return (uint32_t)(16 * lane);   // rows in order: the block's bytes, contiguous
+    const int g = q * 64 + lane, r = g / L::NC, p = g % L::NC;   // the slot's block row and position
+    return (uint32_t)(r * D * 4 + 16 * (p ^ swz<D>(r)) - 1024 * q);   // its source, from the instruction's kilobyte
 }
 
 // this lane's half row of tile `tile` (row ln, dims h*D/2 ..) from a loaded block
@@ -306,15 +336,16 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
     return *reinterpret_cast<const float *>(buf + row * (D * 4) + (((dim >> 2) ^ swz<D>(row)) * 16) + (dim & 3) * 4);
 }
 
-// (64-dim blocks hold 32 KB of rows per wave in LDS, so they run one wave per SIMD: the whole register file.)
+// (64- and 48-dim blocks hold 32 and 24 KB of rows per wave in LDS, and 128 centres take twice the accumulators,
+// so those run one wave per SIMD: the whole register file.)
 //
 // Label state across the passes of a fit (LM): 0 none; 1 every row's label is recorded in lout (one byte per row)
 // and the pass accumulates every row; 2 the pass reads the previous pass's labels (lprev, brought into LDS with
 // the block's rows) and accumulates only the rows whose label changed: +x and +1 for the new cluster, -x and -1
 // for the old one (a signed one-hot), so the partials are the change of the totals since the previous pass; a
 // 64-row block with no changed row skips the accumulation. The inertia is every row's, in every mode.
-template <int D, int KP, int WAVES, bool ACCUM, bool BEST, int LM>
-__global__ __launch_bounds__(64 * WAVES, D >= 64 ? 1 : 2) void k_fused_mfma(
+template <int D, int KP, int WAVES, bool ACCUM, bool BEST, int LM, bool LIST = true>
+__global__ __launch_bounds__(64 * WAVES, (D >= 48 || KP >= 128) ? 1 : 2) void k_fused_mfma(
     const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k,
     uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
     int rb0, km_control *__restrict__ ctl, const uint8_t *__restrict__ lprev, uint8_t *__restrict__ lout,
@@ -349,7 +380,7 @@ __global__ __launch_bounds__(64 * WAVES, D >= 64 ? 1 : 2) void k_fused_mfma(
     constexpr float XSQ_UP = 1.0079f;
     constexpr float XSQ_FLOOR = (float)(G::DP * 0x1p-126);
     constexpr uint32_t IMASK = (1u << G::IB) - 1u;
-    static_assert(D == G::DP && D <= 64 && KP <= 128, "fused kernel serves dims 16, 32, 64 and k <= 128");
+    static_assert(D == G::DP && D <= 64 && KP <= 128, "fused kernel serves dims 16, 32, 48, 64 and k <= 128");
 
     if (stop && *stop) return;
 
@@ -520,7 +551,77 @@ __global__ __launch_bounds__(64 * WAVES, D >= 64 ? 1 : 2) void k_fused_mfma(
         // best +inf included when no distance compares below +inf. The row is read from the block buffer by
         // every lane at one address (a broadcast).
         uint64_t need = __ballot(!unique && valid);
-        if (need) {
+        if (LIST && need && __popcll(need) > KM_SCAN_ROWS) {
+            // ---- many open rows (data whose distances crowd inside the window): each lane rescores its own row
+            // against the centres inside that row's window only. The screen runs again to list them (its values
+            // were not kept), each lane takes its whole row, and the direct form runs over the listed centres in
+            // ascending order with a strict '<' - the rows loop restricted to every centre that can win.
+            asm volatile("" ::: "memory");
+            fallback += (!unique && valid) ? 1u : 0u;
+            const float T2 = T + (4.0f * RHO * fabsf(T) + TINY);
+            const auto tx = __builtin_amdgcn_permlane32_swap(u32(T2), u32(T2), false, false);
+            const float Tp = f32(lane < 32 ? tx[1] : tx[0]);   // the partner lane's threshold
+            const float TA = lane < 32 ? T2 : Tp, TB = lane < 32 ? Tp : T2;   // tile A's row ln, tile B's row ln
+            uint32_t wa[KT], wb[KT], mw[KT];
+            {
+                bf16x8 B[DS];
+                (void)make_b<D, KP>(xa, B);
+                f32x16 a[KT];
+                screen_tile_lds<D, KP>(B, Alds, lane, Acsq, Bone, a);
+                cand_bits<D, KP>(a, TA, h, wa);
+            }
+            {
+                bf16x8 B[DS];
+                (void)make_b<D, KP>(xb, B);
+                f32x16 a[KT];
+                screen_tile_lds<D, KP>(B, Alds, lane, Acsq, Bone, a);
+                cand_bits<D, KP>(a, TB, h, wb);
+            }
+            uint32_t any = 0;
+#pragma unroll
+            for (int t = 0; t < KT; t++) {
+                const auto u = __builtin_amdgcn_permlane32_swap(wa[t], wb[t], false, false);
+                uint32_t m = u[0] | u[1];
+                const int lim = k - 32 * t;
+                if (lim < 32) m &= lim <= 0 ? 0u : ((1u << lim) - 1u);
+                mw[t] = (!unique && valid) ? m : 0u;
+                any |= m;
+            }
+            if (!unique && valid && any == 0) {   // nothing finite in the window (non-finite data): every centre
+#pragma unroll
+                for (int t = 0; t < KT; t++) {
+                    const int lim = k - 32 * t;
+                    mw[t] = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+                }
+            }
+            float lo[DH], hi[DH];
+#pragma unroll
+            for (int q = 0; q < DH; q++) own_halves(xa[q], xb[q], lo[q], hi[q]);
+            if (!unique && valid) {
+                float bv = INFINITY;
+                uint32_t bi = 0;
+#pragma unroll
+                for (int t = 0; t < KT; t++) {
+                    uint32_t wv = mw[t];
+                    while (wv) {
+                        const int c = 32 * t + __builtin_ctz(wv);
+                        wv &= wv - 1u;
+                        const float *cc = Cl + c * CS;
+                        float sc = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < DH; q++) { const float tq = lo[q] - cc[q]; sc = sc + tq * tq; }
+#pragma unroll
+                        for (int q = 0; q < DH; q++) { const float tq = hi[q] - cc[DH + q]; sc = sc + tq * tq; }
+                        if (sc < bv) {
+                            bv = sc;
+                            bi = (uint32_t)c;
+                        }
+                    }
+                }
+                bst = bv;
+                bl = bi;
+            }
+        } else if (need) {
             asm volatile("" ::: "memory");
             fallback += (!unique && valid) ? 1u : 0u;
             do {
@@ -798,22 +899,27 @@ typedef void (*fused_fn)(const float *, int64_t, const float *, int, uint32_t *,
 
 // One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
 // Per block size: the pass without label state, with the rows' exact distances ("b": labels and best outputs),
-// recording the labels ("r"), and accumulating only the rows whose label changed ("i").
+// recording the labels ("r"), accumulating only the rows whose label changed ("i"), and the last without the
+// candidate lists for crowded waves ("s": the whole-wave scan for every open row; a smaller kernel, for data whose
+// open rows are rare).
 struct fused_entry {
     int d, kp;
-    fused_fn acc4, acc4b, acc4r, acc4i, acc2, acc2b, acc2r, acc2i;
+    fused_fn acc4, acc4b, acc4r, acc4i, acc4s, acc2, acc2b, acc2r, acc2i, acc2s;
 };
 
 #define KM_FUSED(DD, KK)                                                                                     \
     {DD, KK, k_fused_mfma<DD, KK, 4, true, false, 0>, k_fused_mfma<DD, KK, 4, true, true, 0>,              \
      k_fused_mfma<DD, KK, 4, true, false, 1>, k_fused_mfma<DD, KK, 4, true, false, 2>,                     \
+     k_fused_mfma<DD, KK, 4, true, false, 2, false>,                                                       \
      k_fused_mfma<DD, KK, 2, true, false, 0>, k_fused_mfma<DD, KK, 2, true, true, 0>,                      \
-     k_fused_mfma<DD, KK, 2, true, false, 1>, k_fused_mfma<DD, KK, 2, true, false, 2>}
+     k_fused_mfma<DD, KK, 2, true, false, 1>, k_fused_mfma<DD, KK, 2, true, false, 2>,                     \
+     k_fused_mfma<DD, KK, 2, true, false, 2, false>}
 
 static fused_entry g_fused[] = {
-    KM_FUSED(16, 32), KM_FUSED(16, 64),
-    KM_FUSED(32, 32), KM_FUSED(32, 64),
-    KM_FUSED(64, 32),
+    KM_FUSED(16, 32), KM_FUSED(16, 64), KM_FUSED(16, 128),
+    KM_FUSED(32, 32), KM_FUSED(32, 64), KM_FUSED(32, 128),
+    KM_FUSED(48, 32), KM_FUSED(48, 64),
+    KM_FUSED(64, 32), KM_FUSED(64, 64),
 };
 #undef KM_FUSED
 
@@ -846,8 +952,8 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
     }
     fused_fn fn = waves == 4 ? fe->acc4 : fe->acc2;
     if (lds > 65536) {
-        const fused_fn all[4] = {fn, waves == 4 ? fe->acc4b : fe->acc2b, waves == 4 ? fe->acc4r : fe->acc2r,
-                                 waves == 4 ? fe->acc4i : fe->acc2i};
+        const fused_fn all[5] = {fn, waves == 4 ? fe->acc4b : fe->acc2b, waves == 4 ? fe->acc4r : fe->acc2r,
+                                 waves == 4 ? fe->acc4i : fe->acc2i, waves == 4 ? fe->acc4s : fe->acc2s};
         for (fused_fn f : all)
             (void)hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
@@ -872,14 +978,15 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
 
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
-                          const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s) {
+                          const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s,
+                          int scan_only) {
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
     if (lmode != 0 && (want_best || !lout || (lmode == 2 && !lprev))) return hipErrorInvalidValue;
     const bool w4 = pl.waves == 4;
     fused_fn fn = want_best ? (w4 ? fe->acc4b : fe->acc2b)
                   : lmode == 1 ? (w4 ? fe->acc4r : fe->acc2r)
-                  : lmode == 2 ? (w4 ? fe->acc4i : fe->acc2i)
+                  : lmode == 2 ? (scan_only ? (w4 ? fe->acc4s : fe->acc2s) : (w4 ? fe->acc4i : fe->acc2i))
                                : (w4 ? fe->acc4 : fe->acc2);
     hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, labels, best, psum,
                        pcomp, rb0, ctl, lprev, lout, stop);

@@ -33,9 +33,9 @@ def lib():
 
 
 def mfma_served(d, k):
-    """The fused screen serves d = 16, 32 with k <= 64 and d = 64 with k <= 32; the wide-row screen serves
+    """The fused screen serves d = 16, 32 with k <= 128 and d = 48, 64 with k <= 64; the wide-row screen serves
     16 < d <= 1536 with k <= 4096."""
-    return d in (16, 32) and k <= 64 or d == 64 and k <= 32 or 16 < d <= 1536 and k <= 4096
+    return d in (16, 32) and k <= 128 or d in (48, 64) and k <= 64 or 16 < d <= 1536 and k <= 4096
 
 
 def fused_served(d, k):
@@ -158,6 +158,59 @@ def test_paths_are_bit_identical(lib, d, k):
         cnt = np.maximum(np.rint(t1[:, 0]), 1)[:, None]
         assert np.max(np.abs(t1[:, 2:] - t2[:, 2:]) / cnt) / scale <= CENTRE_TOL, name
         np.testing.assert_allclose(t2[:, 1], t1[:, 1], rtol=1e-6, atol=1e-30)
+    ctx.close()
+
+
+@pytest.mark.parametrize("d,k", [(48, 64), (48, 41), (48, 20), (64, 64), (64, 47), (32, 128), (32, 97),
+                                 (16, 128), (16, 72)])
+def test_fused_mfma_shapes_match_oracle(lib, d, k):
+    """The fused matrix-core pass on the shapes of the reference's one-hot domain beyond 16-64 dims with 64
+    centres (core.py:1639-1646: k <= 128, d <= 96): 48-dim rows (kept in order in LDS), 64 dims with up to 64
+    centres and 128 centres at 16 and 32 dims, over two uneven slices with duplicate centres and non-finite rows.
+    Labels and best bit-identical to the oracle, counts exact, sums and inertia within tolerance, the fused
+    kernel (not the wide-row screen) the one that ran, and a fit whose change-only passes match single steps."""
+    import oracle
+    rng = np.random.default_rng(900 + 7 * d + k)
+    n = 70_001
+    cen = rng.uniform(-3, 3, size=(max(k // 2, 2), d)).astype(np.float32)
+    X = (cen[rng.integers(0, len(cen), n)] + 0.7 * rng.standard_normal((n, d))).astype(np.float32)
+    C = X[rng.choice(n, k, replace=False)].copy()
+    C[k - 1] = C[1]                               # duplicate centres: ties go to index 1
+    X[100:110] = C[1]
+    X[7] = np.nan
+    X[8, d // 2] = np.inf
+    parts = [X[:30_017], X[30_017:]]
+    scale = float(np.sqrt((X[np.isfinite(X).all(1)].astype(np.float64) ** 2).mean()))
+    ctx = lib.Context()
+    ctx.set_parts(parts)
+    say(f"[gpu] fused mfma shape d={d} k={k}")
+    ctx.profile(True)
+    tot, labels, best = ctx.run_pass(C, path=lib.KM_PATH_MFMA, labels=True, best=True)
+    ran = ctx.profile_read()
+    ctx.profile(False)
+    assert "km_fused_mfma" in ran and "km_big_screen" not in ran, ran
+    ol, ob = oracle.assign(X, C)
+    assert np.array_equal(labels, ol), np.flatnonzero(labels != ol)[:10]
+    assert np.array_equal(best.view(np.uint32), ob.view(np.uint32))
+    assert np.array_equal(np.rint(tot[:, 0]).astype(np.int64), np.bincount(ol, minlength=k))
+    ctx.close()
+    fin = np.isfinite(X).all(1)
+    # the fit loop on finite rows: change-only passes against one-at-a-time full steps
+    Xf = X[fin]
+    ctx = lib.Context()
+    ctx.set_parts([Xf[:40_003], Xf[40_003:]] if d != 64 else [Xf])
+    tot1, l1, b1 = ctx.run_pass(C, labels=True, best=True)
+    check_totals(tot1, Xf, l1, b1, oracle.totals(Xf, *oracle.assign(Xf, C), k), scale)
+    Cs = C.copy()
+    for _ in range(6):
+        Cs, _, _ = ctx.lloyd_step(Cs)
+    Cf, inf, it, _ = ctx.fit(C, 6, -1.0)
+    assert it == 6
+    assert float(np.max(np.abs(Cf.astype(np.float64) - Cs))) / scale <= CENTRE_TOL
+    # a second fit on the context: its change-only passes may take the kernel without candidate lists (chosen
+    # from the open rows the first fit saw); the result is the first fit's, bit for bit
+    Cg, ing, _, _ = ctx.fit(C, 6, -1.0)
+    assert np.array_equal(Cg.view(np.uint32), Cf.view(np.uint32)) and ing == inf
     ctx.close()
 
 

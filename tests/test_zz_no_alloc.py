@@ -117,7 +117,8 @@ def _data(seed, n, d, k):
 # (dims, centres, rows of the two calls): the fused matrix-core, fused low-d and rows families, the rows loop's
 # tiled form (d = 100, k = 64), and a shape km_pass sends to the wide-row screen while the allocation-free pass
 # runs the tiled rows loop over as few row blocks as its scratch holds (d = 768, k = 256)
-@pytest.mark.parametrize("d,k,ns", [(32, 64, (120_011, 33_007)), (4, 12, (120_011, 33_007)),
+@pytest.mark.parametrize("d,k,ns", [(32, 64, (120_011, 33_007)), (48, 64, (90_011, 33_007)),
+                                    (32, 128, (90_011, 33_007)), (4, 12, (120_011, 33_007)),
                                     (16, 40, (120_011, 33_007)), (48, 100, (120_011, 33_007)),
                                     (3, 300, (120_011, 33_007)), (100, 64, (50_011, 20_007)),
                                     (768, 256, (20_011, 9_007))])
