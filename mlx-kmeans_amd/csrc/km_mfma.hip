@@ -98,8 +98,8 @@ struct Geo {
     static constexpr int AK = DS + 1;               // A-operand K-steps: bf16(-2c), then |c|^2
     static constexpr int KT = KP / 32;              // centre tiles
     static constexpr int IB = KT <= 1 ? 4 : KT <= 2 ? 5 : 6;   // index bits packed into keys (16 KT values)
-    static constexpr int CS = D + 1;                // LDS row stride of the float32 centres (odd: lanes reading
-                                                    // different centres' rows hit different banks)
+    static constexpr int CS = DP + 1;               // LDS row stride of the float32 centres, zero past D (odd:
+                                                    // lanes reading different centres' rows hit different banks)
     static constexpr int AS = D + 1;                // LDS row stride of the accumulators
 };
 
@@ -313,16 +313,20 @@ __device__ __forceinline__ uint32_t issue_voff(int lane, int q) {
     return (uint32_t)(r * D * 4 + 16 * (p ^ swz<D>(r)) - 1024 * q);   // its source, from the instruction's kilobyte
 }
 
-// this lane's half row of tile `tile` (row ln, dims h*D/2 ..) from a loaded block
+// this lane's half row of tile `tile` (row ln, dims h DP/2 .. of the dims padded to DP, a multiple of 16; the
+// dims past D read as zeros) from a loaded block
 template <int D>
-__device__ __forceinline__ void read_half(const char *buf, int tile, int lane, float (&x)[D / 2]) {
+__device__ __forceinline__ void read_half(const char *buf, int tile, int lane, float (&x)[(D + 15) / 16 * 8]) {
     using L = Lay<D>;
+    constexpr int QH = (D + 15) / 16 * 2;   // chunks per padded half row
     const int ln = lane & 31, h = lane >> 5;
     const int r = 32 * tile + ln, sw = swz<D>(r);
     const char *row = buf + r * (D * 4);
 #pragma unroll
-    for (int q = 0; q < L::QI; q++) {
-        const float4 v = *reinterpret_cast<const float4 *>(row + ((h * L::QI + q) ^ sw) * 16);
+    for (int q = 0; q < QH; q++) {
+        const int c = h * QH + q;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (D == (D + 15) / 16 * 16 || c < L::NC) v = *reinterpret_cast<const float4 *>(row + (c ^ sw) * 16);
         x[4 * q] = v.x;
         x[4 * q + 1] = v.y;
         x[4 * q + 2] = v.z;
@@ -336,8 +340,8 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
     return *reinterpret_cast<const float *>(buf + row * (D * 4) + (((dim >> 2) ^ swz<D>(row)) * 16) + (dim & 3) * 4);
 }
 
-// (64- and 48-dim blocks hold 32 and 24 KB of rows per wave in LDS, and 128 centres take twice the accumulators,
-// so those run one wave per SIMD: the whole register file.)
+// (Above 32 dims a wave holds 20-32 KB of rows in LDS and two accumulator tiles per centre tile, and 128 centres
+// take twice the accumulators, so those run one wave per SIMD: the whole register file.)
 //
 // Label state across the passes of a fit (LM): 0 none; 1 every row's label is recorded in lout (one byte per row)
 // and the pass accumulates every row; 2 the pass reads the previous pass's labels (lprev, brought into LDS with
@@ -345,7 +349,7 @@ __device__ __forceinline__ float read_elem(const char *buf, int row, int dim) {
 // for the old one (a signed one-hot), so the partials are the change of the totals since the previous pass; a
 // 64-row block with no changed row skips the accumulation. The inertia is every row's, in every mode.
 template <int D, int KP, int WAVES, bool ACCUM, bool BEST, int LM, bool LIST = true>
-__global__ __launch_bounds__(64 * WAVES, (D >= 48 || KP >= 128) ? 1 : 2) void k_fused_mfma(
+__global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_fused_mfma(
     const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k,
     uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
     int rb0, km_control *__restrict__ ctl, const uint8_t *__restrict__ lprev, uint8_t *__restrict__ lout,
@@ -380,7 +384,7 @@ __global__ __launch_bounds__(64 * WAVES, (D >= 48 || KP >= 128) ? 1 : 2) void k_
     constexpr float XSQ_UP = 1.0079f;
     constexpr float XSQ_FLOOR = (float)(G::DP * 0x1p-126);
     constexpr uint32_t IMASK = (1u << G::IB) - 1u;
-    static_assert(D == G::DP && D <= 64 && KP <= 128, "fused kernel serves dims 16, 32, 48, 64 and k <= 128");
+    static_assert(D % 8 == 0 && D <= 64 && KP <= 128, "fused kernel serves dims 16-64 (multiples of 8), k <= 128");
 
     if (stop && *stop) return;
 
@@ -917,8 +921,11 @@ struct fused_entry {
 
 static fused_entry g_fused[] = {
     KM_FUSED(16, 32), KM_FUSED(16, 64), KM_FUSED(16, 128),
+    KM_FUSED(24, 32), KM_FUSED(24, 64), KM_FUSED(24, 128),
     KM_FUSED(32, 32), KM_FUSED(32, 64), KM_FUSED(32, 128),
+    KM_FUSED(40, 32), KM_FUSED(40, 64),
     KM_FUSED(48, 32), KM_FUSED(48, 64),
+    KM_FUSED(56, 32), KM_FUSED(56, 64),
     KM_FUSED(64, 32), KM_FUSED(64, 64),
 };
 #undef KM_FUSED
@@ -929,7 +936,7 @@ static size_t lds_for(int d, int kp, int waves) {
     const size_t loop = 2 * ((size_t)(64 * d * 4) + 64) + 256 + 4 * (size_t)kp;
     const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float) + 4 * (size_t)kp;
     const size_t abytes = (size_t)(kp / 32) * ((d + 15) / 16) * 64 * 16;
-    return (size_t)kp * (d + 1) * sizeof(float) + abytes + waves * (loop > fold ? loop : fold);
+    return (size_t)kp * ((d + 15) / 16 * 16 + 1) * sizeof(float) + abytes + waves * (loop > fold ? loop : fold);
 }
 
 static const fused_entry *find_fused(int d, int k) {

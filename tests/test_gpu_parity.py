@@ -33,9 +33,10 @@ def lib():
 
 
 def mfma_served(d, k):
-    """The fused screen serves d = 16, 32 with k <= 128 and d = 48, 64 with k <= 64; the wide-row screen serves
-    16 < d <= 1536 with k <= 4096."""
-    return d in (16, 32) and k <= 128 or d in (48, 64) and k <= 64 or 16 < d <= 1536 and k <= 4096
+    """The fused screen serves d = 16, 24, 32 with k <= 128 and d = 40, 48, 56, 64 with k <= 64; the wide-row screen
+    serves 16 < d <= 1536 with k <= 4096."""
+    return (d in (16, 24, 32) and k <= 128 or d in (40, 48, 56, 64) and k <= 64
+            or 16 < d <= 1536 and k <= 4096)
 
 
 def fused_served(d, k):
@@ -162,11 +163,13 @@ def test_paths_are_bit_identical(lib, d, k):
 
 
 @pytest.mark.parametrize("d,k", [(48, 64), (48, 41), (48, 20), (64, 64), (64, 47), (32, 128), (32, 97),
-                                 (16, 128), (16, 72)])
+                                 (16, 128), (16, 72), (24, 128), (24, 64), (24, 20), (40, 64), (40, 17), (56, 64),
+                                 (56, 33)])
 def test_fused_mfma_shapes_match_oracle(lib, d, k):
     """The fused matrix-core pass on the shapes of the reference's one-hot domain beyond 16-64 dims with 64
-    centres (core.py:1639-1646: k <= 128, d <= 96): 48-dim rows (kept in order in LDS), 64 dims with up to 64
-    centres and 128 centres at 16 and 32 dims, over two uneven slices with duplicate centres and non-finite rows.
+    centres (core.py:1639-1646: k a multiple of 8 up to 128, d up to 96): 24-, 40-, 48- and 56-dim rows (kept in
+    order in LDS; 24, 40 and 56 padded to 32, 48 and 64 in the screen), 64 dims with up to 64 centres and 128
+    centres at 16, 24 and 32 dims, over two uneven slices with duplicate centres and non-finite rows.
     Labels and best bit-identical to the oracle, counts exact, sums and inertia within tolerance, the fused
     kernel (not the wide-row screen) the one that ran, and a fit whose change-only passes match single steps."""
     import oracle
