@@ -35,6 +35,9 @@ DESCRIPTIONS = {
     "embed_d768": "1M x 768 fp32, k=1024, unit-norm vMF-style embeddings",
     "embed_d1536": "1M x 1536 fp32, k=1024, unit-norm vMF-style embeddings",
     "blobs_d960": "1M x 960 fp32, k=1024, GIST-width 1024-blob mixture, k-means++ start",
+    "blobs_d48": "10M x 48 fp32, k=64, 64-component mixture, k-means++ start",
+    "blobs_d32_k128": "10M x 32 fp32, k=128, 128-component mixture, k-means++ start",
+    "blobs_d96": "10M x 96 fp32, k=64, 64-component mixture, k-means++ start",
 }
 
 

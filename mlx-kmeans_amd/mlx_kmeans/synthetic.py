@@ -12,6 +12,11 @@
     embed_d768     1M x 768, k=1024: unit rows normalize(centre + N(0, 0.15^2 I)) around 1024 random unit
                    centres; start: 1024 seeded rows; 15 iterations
     embed_d1536    the same at 1536 dims (the widest rows the matrix-core screen takes)
+    blobs_d48      10M x 48, k=64 \
+    blobs_d32_k128 10M x 32, k=128 } blobs_d32's mixture (means ~U[-10,10]^d, sigma 1, one component per centre) at
+    blobs_d96      10M x 96, k=64 /  the widths and centre counts of the reference's one-hot domain (core.py:1639-1646;
+                   d = 96 with k = 64 lies past its k (d / 8 + 1) <= 640); start: k-means++ on a 10k-row subsample;
+                   20 iterations
     blobs_d960     1M x 960, k=1024: GIST-like width, 1024-component isotropic mixture, means ~U[-1,1]^960, sigma 1
                    (the reference's bounds sequence, tests/accuracy.py:305-306, at 1M rows and one blob per
                    centre); start: greedy k-means++ on a 20,480-row subsample; 20 iterations. Well separated: the
@@ -109,6 +114,25 @@ def outliers_d32(n=10_000_000, seed=0):
     return dict(name="outliers_d32", X=X, C0=C0, k=64, iters=20)
 
 
+def _onehot_blobs(name, n, d, k, seed):
+    rng = np.random.default_rng(seed)
+    X = _blobs(rng, n, d, k, 10.0)
+    C0 = kmeans_pp_init([X], n, k, rng, sample=10_000)
+    return dict(name=name, X=X, C0=C0, k=k, iters=20)
+
+
+def blobs_d48(n=10_000_000, seed=0):
+    return _onehot_blobs("blobs_d48", n, 48, 64, seed)
+
+
+def blobs_d32_k128(n=10_000_000, seed=0):
+    return _onehot_blobs("blobs_d32_k128", n, 32, 128, seed)
+
+
+def blobs_d96(n=10_000_000, seed=0):
+    return _onehot_blobs("blobs_d96", n, 96, 64, seed)
+
+
 def pixels_d4(n=96_000_000, seed=0):
     rng = np.random.default_rng(seed)
     k, d = 12, 4
@@ -174,4 +198,7 @@ WORKLOADS = {
     "embed_d768": embed_d768,
     "embed_d1536": embed_d1536,
     "blobs_d960": blobs_d960,
+    "blobs_d48": blobs_d48,
+    "blobs_d32_k128": blobs_d32_k128,
+    "blobs_d96": blobs_d96,
 }
