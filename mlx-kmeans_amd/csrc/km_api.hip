@@ -738,8 +738,6 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         }
         int r = ensure_pass_buffers(c, k, total_rb, false);
         if (r) return r;
-        // where the last fit saw few open rows, its change-only passes take the kernel without candidate lists
-        const int scan_only = lmode == KM_LSTATE_DELTA && c->open_frac >= 0.0 && c->open_frac <= KM_SCAN_ONLY_FRAC;
         int rb = 0;
         int64_t row0 = 0;
         for (size_t i = 0; i < c->parts.size(); i++) {
