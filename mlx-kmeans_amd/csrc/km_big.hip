@@ -371,13 +371,25 @@ __device__ __forceinline__ void kb_screen_tile(
                     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Ab[j % (PF + 1)], s < DS ? B[s < DS ? s : 0] : Bone,
                                                                    acc, 0, 0, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);   // PF LDS reads,
+            // the chunk's last slice may hold fewer K-steps (LAST): its groups are counted from its own length
+            constexpr int LAST = AK - (SPC - 1) * SLK, PFL = PF < LAST ? PF : LAST;
+            if (sl + 1 < SPC || LAST == SLK) {
+                __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);   // PF LDS reads,
 #pragma unroll
-            for (int j = 0; j < SLK - PF; j++) {                    // then MFMA, LDS read, ...,
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int j = 0; j < SLK - PF; j++) {                    // then MFMA, LDS read, ...,
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);   // and the last PF MFMAs
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x100, PFL, 0);
+#pragma unroll
+                for (int j = 0; j < LAST - PFL; j++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, PFL, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);   // and the last PF MFMAs
         }
     };
 
