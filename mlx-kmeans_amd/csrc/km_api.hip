@@ -572,7 +572,7 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
     HIPCHK(c, c->bcn.ensure((size_t)bp0.kpad * 2));
     HIPCHK(c, c->bmax.ensure(4));
     HIPCHK(c, c->ncand.ensure((size_t)max_rows));
-    HIPCHK(c, c->cand.ensure((size_t)max_rows * 32));
+    HIPCHK(c, c->cand.ensure((size_t)max_rows * 2 * km_big_list_slot(d)));
     HIPCHK(c, c->hist.ensure((size_t)max_nb * k));
     HIPCHK(c, c->counts.ensure((size_t)k));
     HIPCHK(c, c->base.ensure((size_t)k));
@@ -641,8 +641,8 @@ static int run_big(km_ctx *c, int k, int mode, uint32_t *labels_d, float *best_d
             }));
             HIPCHK(c, launch(c, KK_BOUNDS_LIST, [&] {
                 return km_launch_bnd_list(lb, bref.ub, bref.ubl, p.rows, k, bp.nchunks, c->bnd_S.p, c->bnd_delta.p,
-                                          km_bnd_hi(d), c->ncand.p, c->cand.p, c->over.p, c->multi.p, c->ctl, bs,
-                                          c->dev.cus, c->stream);
+                                          km_bnd_hi(d), c->ncand.p, c->cand.p, km_big_list_slot(d), c->over.p,
+                                          c->multi.p, c->ctl, bs, c->dev.cus, c->stream);
             }));
         }
         HIPCHK(c, launch(c, KK_BIG_RESCORE, [&] {

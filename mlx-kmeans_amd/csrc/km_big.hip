@@ -10,9 +10,9 @@
 //                   over the centres: the row's smallest packed key (value, centre index) so far, and the centres
 //                   inside the error window around it - every centre that can hold the exact minimum
 //   k_big_rescore   the rows loop (core.py:263-274) on those candidates only, ascending index, strict '<'
-//   k_big_fullscan  rows whose window holds more than 16 centres of one half-row (or non-finite data): every
-//                   centre, 64 rows x 64 centres per block step; without a row list, every row of a part (the
-//                   rows loop's tiled form, km_launch_rows_tiled)
+//   k_big_fullscan  rows whose window holds more centres of one half-row than its list takes (16; 32 above 768
+//                   dims) or non-finite data: every centre, 64 rows x 64 centres per block step; without a row
+//                   list, every row of a part (the rows loop's tiled form, km_launch_rows_tiled)
 //   k_big_hist/scan/scatter   a stable counting sort of the rows by label; then the per-cluster float64 sums in
 //                   row order, in fixed chunks of sorted rows (km_chunks.hip): the totals of the pass
 //
@@ -35,8 +35,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float kb_f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int kb_u4 __attribute__((ext_vector_type(4)));
 
-static constexpr int KB_HALF = 16;        // candidates kept per half-row lane
-static constexpr int KB_CAP = 2 * KB_HALF; // candidates kept per row
+// candidates a half-row's list holds: 16, and 32 above 48 K-steps (769 dims and wider, where a row's window crowds
+// more centres; one screen block per CU leaves the LDS for it). The global lists hold 2 kb_list_half(DS) slots per
+// row, the half-rows' lists at slots 0 and kb_list_half(DS).
+__host__ __device__ constexpr int kb_list_half(int DS) { return DS > 48 ? 32 : 16; }
+static constexpr int KB_LIST_MAX = 32;    // the longest half-row list
 static constexpr int KB_SLICE = 25;       // most A-operand K-steps per LDS slice (1 KB each): 768 dims take two
                                           // slices per chunk, so two block barriers and a prefetch of half a chunk
 // Above 48 K-steps one block per CU has the LDS to itself: slices of up to 49 K-steps, two per chunk (500k x 960 /
@@ -252,7 +255,8 @@ __global__ __launch_bounds__(256) void k_big_centres(const float *__restrict__ C
 // absorbed by the test. The window only narrows as the row's smallest key falls, so the screen lists, chunk by
 // chunk, every centre inside the window of the smallest key seen so far, prunes a full list against the current
 // window, and at the end keeps the listed centres inside the final window - exactly the centres the final window
-// admits. A half-row with more than KB_HALF of them at once (or non-finite data) sends the row to a full scan.
+// admits. A half-row with more than kb_list_half(DS) of them at once (16 up to 768 dims, 32 above), or non-finite
+// data, sends the row to a full scan.
 
 // The window's error bound E for a row (see above) with DS K-steps, from its |x|^2 (rounded up), |bf16(x) - x| and
 // the centres' maxes {max |c|, max |c|^2, max |f|}; nx gets |x| rounded up.
@@ -294,6 +298,7 @@ __device__ __forceinline__ void kb_screen_tile(
     const uint16_t *__restrict__ Cop, const float *__restrict__ maxes, int k, int nchunks, int ib, float rho,
     int approx, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand, uint32_t *__restrict__ over,
     uint32_t *__restrict__ multi, km_control *__restrict__ ctl, const kb_bnd_out &bnd) {
+    constexpr int LH = kb_list_half(DS);   // this width's list length per half-row
     constexpr int DP = 16 * DS, AK = DS + 1;
     constexpr float TINY = (float)((DP + 2) * 0x1p-118);
     extern __shared__ float lds[];
@@ -412,14 +417,14 @@ __device__ __forceinline__ void kb_screen_tile(
         return (T < INFINITY) ? Tp : -INFINITY;
     };
     // One pass over the centre chunks. Per chunk: the row's smallest key so far (both halves), its key bound, and
-    // this chunk's keys inside it appended to this lane's list in LDS (up to KB_HALF; a full list is first pruned
+    // this chunk's keys inside it appended to this lane's list in LDS (up to LH; a full list is first pruned
     // against the current bound, and if still full the row takes the full scan). Approximate mode keeps only the
     // smallest key.
-    float *list = reinterpret_cast<float *>(ring + 2 * SLK * 1024) + (size_t)wave * KB_HALF * 64 + lane;
+    float *list = reinterpret_cast<float *>(ring + 2 * SLK * 1024) + (size_t)wave * LH * 64 + lane;
     // without packed keys, the listed keys' centre indices (after the KB_WAVES lists of keys)
     uint16_t *lidx = reinterpret_cast<uint16_t *>(reinterpret_cast<float *>(ring + 2 * SLK * 1024) +
-                                                  (size_t)KB_WAVES * KB_HALF * 64) +
-                     (size_t)wave * KB_HALF * 64 + lane;
+                                                  (size_t)KB_WAVES * LH * 64) +
+                     (size_t)wave * LH * 64 + lane;
     // a sample tile of the per-centre bounds (32-bit arithmetic: a slice has fewer than 2^27 tiles)
     const bool sample = !BND && bnd.sraw && have && (uint32_t)tile % (uint32_t)bnd.sstride == 0u;
     float *sdst = sample ? bnd.sraw + ((int64_t)((uint32_t)tile / (uint32_t)bnd.sstride) * nchunks * 64 + lane) * 16
@@ -473,9 +478,9 @@ __device__ __forceinline__ void kb_screen_tile(
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 if ((bal[v] >> lane) & 1ull) {
-                    if (cnt == KB_HALF && !spill) {   // full: drop what the current bound already excludes
+                    if (cnt == LH && !spill) {   // full: drop what the current bound already excludes
                         int w = 0;
-                        for (int q = 0; q < KB_HALF; q++) {
+                        for (int q = 0; q < LH; q++) {
                             const float kq = list[q * 64];
                             if (kq <= Tp) {
                                 if (!PACK) lidx[w * 64] = lidx[q * 64];
@@ -483,9 +488,9 @@ __device__ __forceinline__ void kb_screen_tile(
                             }
                         }
                         cnt = w;
-                        spill = cnt == KB_HALF;
+                        spill = cnt == LH;
                     }
-                    if (cnt < KB_HALF) {
+                    if (cnt < LH) {
                         if (!PACK) lidx[cnt * 64] = (uint16_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
                         list[(cnt++) * 64] = key[v];
                     }
@@ -502,16 +507,16 @@ __device__ __forceinline__ void kb_screen_tile(
         for (int q = 0; q < cnt; q++) {
             const float kq = list[q * 64];
             if (kq <= Tp && (!BND || bnd.lists))
-                cand[row * KB_CAP + h * KB_HALF + (w++)] = PACK ? (uint16_t)(kb_u32(kq) & IMASK) : lidx[q * 64];
+                cand[row * (2 * LH) + h * LH + (w++)] = PACK ? (uint16_t)(kb_u32(kq) & IMASK) : lidx[q * 64];
         }
         cnt = w;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (!real_row) return;
-    // The other half-row's count, or KB_HALF + 1 when its list overflowed: a lane's count never exceeds KB_HALF
+    // The other half-row's count, or LH + 1 when its list overflowed: a lane's count never exceeds LH
     // (the final filter only lowers it), so the overflow has to travel as its own value.
-    const int cnt_o = (int)kb_f32u(kb_partner(kb_u32f((uint32_t)(spill ? KB_HALF + 1 : cnt)), lane));
-    const bool spill_o = cnt_o > KB_HALF;
+    const int cnt_o = (int)kb_f32u(kb_partner(kb_u32f((uint32_t)(spill ? LH + 1 : cnt)), lane));
+    const bool spill_o = cnt_o > LH;
     if (h != 0) return;
     if (BND) {   // an upper bound on the distance to the minimiser m (D_m <= |x|^2 + a'_m + E), and m
         float u = INFINITY;
@@ -527,7 +532,7 @@ __device__ __forceinline__ void kb_screen_tile(
     if (!finite) {
         code = KB_OVER;   // non-finite data: the rows loop decides
     } else if (approx) {
-        cand[row * KB_CAP] = (uint16_t)(kb_u32(m1) & IMASK);
+        cand[row * (2 * LH)] = (uint16_t)(kb_u32(m1) & IMASK);
         code = 1;
     } else if (spill || spill_o || cnt + cnt_o == 0) {
         code = KB_OVER;   // an empty window cannot happen for finite data (the minimiser is inside it)
@@ -607,7 +612,7 @@ template <bool V4, bool LITE>
 __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__ X, int64_t n, int d,
                                                        const float *__restrict__ C, int k,
                                                        const uint16_t *__restrict__ ncand,
-                                                       const uint16_t *__restrict__ cand,
+                                                       const uint16_t *__restrict__ cand, int slot,
                                                        const uint32_t *__restrict__ list,
                                                        const km_control *__restrict__ ctl,
                                                        uint32_t *__restrict__ labels, float *__restrict__ best,
@@ -619,9 +624,9 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
     __shared__ uint32_t rid[KB_RR];   // the block's rows: consecutive, or entries of the list
     __shared__ float xs[KB_RR * (KB_RCH + 1)];
     __shared__ float cs[KB_RT * (KB_RCH + 1)];
-    __shared__ uint16_t it_c[KB_RR * KB_CAP];
-    __shared__ uint8_t it_r[KB_RR * KB_CAP];
-    __shared__ float it_s[KB_RR * KB_CAP];
+    __shared__ uint16_t it_c[KB_RR * 2 * KB_LIST_MAX];
+    __shared__ uint8_t it_r[KB_RR * 2 * KB_LIST_MAX];
+    __shared__ float it_s[KB_RR * 2 * KB_LIST_MAX];
     __shared__ int first[KB_RR + 1];
     const int tid = threadIdx.x, lane = tid & 63;
     const int64_t total = LITE ? (int64_t)ctl->n_multi : n;
@@ -652,7 +657,7 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         for (int half = 0; half < 2; half++) {
             const int nc = half ? code >> 8 : code & 255;
             for (int i = 0; i < nc; i++) {
-                const uint16_t v = cand[(int64_t)rid[tid] * KB_CAP + half * KB_HALF + i];
+                const uint16_t v = cand[(int64_t)rid[tid] * (2 * slot) + half * slot + i];
                 int j = m - 1;
                 while (j >= b && it_c[j] > v) { it_c[j + 1] = it_c[j]; j--; }
                 it_c[j + 1] = v;
@@ -804,16 +809,16 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
 // Labels of the rows whose window held a single candidate (passes without per-row distances; the rescoring
 // takes the listed rows with several).
 __global__ __launch_bounds__(256) void k_big_label1(const uint16_t *__restrict__ ncand, const uint16_t *__restrict__ cand,
-                                                    int64_t n, uint32_t *__restrict__ labels,
+                                                    int64_t n, int slot, uint32_t *__restrict__ labels,
                                                     const int32_t *__restrict__ stop) {
     if (stop && *stop) return;
     const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (r >= n) return;
     const int code = ncand[r];
-    if (code != KB_OVER && (code & 255) + (code >> 8) == 1) labels[r] = cand[r * KB_CAP + ((code & 255) ? 0 : KB_HALF)];
+    if (code != KB_OVER && (code & 255) + (code >> 8) == 1) labels[r] = cand[r * (2 * slot) + ((code & 255) ? 0 : slot)];
 }
 
-// Rows the screen could not narrow (more than KB_HALF window centres in a half-row, or non-finite data) take the
+// Rows the screen could not narrow (more than kb_list_half window centres in a half-row, or non-finite data) take the
 // rows loop over every centre. Blocks of 256 threads take 64 listed rows at a time against chunks of 64 centres:
 // 32 dims of the rows and of the centres staged in LDS per step, each thread carrying 4 rows x 4 centres of
 // direct-form sums (dims ascending, product and add rounded separately) across the steps, then keeping per row
@@ -1172,6 +1177,8 @@ km_big_plan km_plan_big(int64_t n, int d, int k) {
     return pl;
 }
 
+int km_big_list_slot(int d) { return kb_list_half(kb_ds(d)); }
+
 size_t km_big_x16_elems(const km_big_plan &pl) { return (size_t)pl.ntiles * pl.DS * 64 * 8; }
 size_t km_big_cop_elems(const km_big_plan &pl) { return (size_t)pl.nchunks * (pl.DS + 1) * 64 * 8; }
 
@@ -1218,7 +1225,7 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
     // below 64 dims the reference's dispatch runs its exact kernels (core.py:2036-2042)
     const int approx = (mode == KM_APPROX && d >= KM_APPROX_MIN_DIMS) ? 1 : 0;
     const int ak = pl.DS + 1, spc = (ak + kb_slice(pl.DS) - 1) / kb_slice(pl.DS), slk = (ak + spc - 1) / spc;
-    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * KB_HALF * 64 * (pack ? 4 : 6);
+    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * kb_list_half(pl.DS) * 64 * (pack ? 4 : 6);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
@@ -1238,19 +1245,20 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
     const km_bnd_refresh br = bref ? *bref : km_bnd_refresh{};
     hipError_t e;
     typedef void (*rescore_fn)(const float *, int64_t, int, const float *, int, const uint16_t *, const uint16_t *,
-                               const uint32_t *, const km_control *, uint32_t *, float *, const int32_t *,
+                               int, const uint32_t *, const km_control *, uint32_t *, float *, const int32_t *,
                                km_bnd_refresh);
+    const int slot = km_big_list_slot(d);
     if (lite) {
-        hipLaunchKernelGGL(k_big_label1, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ncand, cand, n, labels,
-                           stop);
+        hipLaunchKernelGGL(k_big_label1, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ncand, cand, n, slot,
+                           labels, stop);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         const rescore_fn fn = v4 ? k_big_rescore<true, true> : k_big_rescore<false, true>;
         hipLaunchKernelGGL(fn, dim3(chunks < 4096u ? chunks : 4096u), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
-                           multi, ctl, labels, best, stop, br);
+                           slot, multi, ctl, labels, best, stop, br);
     } else {
         const rescore_fn fn = v4 ? k_big_rescore<true, false> : k_big_rescore<false, false>;
-        hipLaunchKernelGGL(fn, dim3(chunks), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand, (const uint32_t *)nullptr,
-                           ctl, labels, best, stop, br);
+        hipLaunchKernelGGL(fn, dim3(chunks), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand, slot,
+                           (const uint32_t *)nullptr, ctl, labels, best, stop, br);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (k <= KB_FSPLIT || !okeys) {
@@ -1276,7 +1284,7 @@ static hipError_t kb_launch_screen_bnd(const km_big_plan &pl, const uint16_t *X1
                                        uint16_t *lb, float *ub, uint32_t *ubl, km_bnd *bs, int cus, hipStream_t s) {
     const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
     const int ak = DS + 1, spc = (ak + kb_slice(DS) - 1) / kb_slice(DS), slk = (ak + spc - 1) / spc;
-    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * KB_HALF * 64 * 4;
+    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * kb_list_half(DS) * 64 * 4;
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)k_big_screen_bnd<DS>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);

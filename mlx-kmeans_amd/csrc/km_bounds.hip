@@ -37,8 +37,6 @@
 
 namespace {
 
-constexpr int KD_HALF = 16;              // candidates per half-row (the screen's KB_HALF)
-constexpr int KD_CAP = 2 * KD_HALF;      // per row
 constexpr int KD_OVER = 0xffff;          // ncand: scan every centre
 
 typedef _Float16 kd_h8 __attribute__((ext_vector_type(8)));
@@ -52,13 +50,13 @@ __device__ __forceinline__ float kd_raise(float u, float dl, float hi) {
 
 // Wave per 32-row tile, lane per half-row (row 32 t + lane % 32, centres of half lane / 32 of each chunk, the
 // screen's order): every centre c with lb_c - S_c not above ub goes to the row's candidate lists (as the screen
-// writes them: at most KD_HALF per half-row, else the row takes the full scan, as does a row without a finite ub),
+// writes them: at most `slot` per half-row, else the row takes the full scan, as does a row without a finite ub),
 // and the raised ub is written back.
 __global__ __launch_bounds__(256) void k_bnd_list(const uint16_t *__restrict__ lb, float *__restrict__ ub,
                                                   const uint32_t *__restrict__ ubl, int64_t n, int k, int nchunks,
                                                   const float *__restrict__ S, const float *__restrict__ delta,
                                                   float hi, uint16_t *__restrict__ ncand, uint16_t *__restrict__ cand,
-                                                  uint32_t *__restrict__ over, uint32_t *__restrict__ multi,
+                                                  int slot, uint32_t *__restrict__ over, uint32_t *__restrict__ multi,
                                                   km_control *__restrict__ ctl, const int32_t *__restrict__ gate) {
     if (*gate) return;
     extern __shared__ float Sp[];   // S in the screen's order: Sp[32 ch + 16 h + v] = S[km_bnd_centre(ch, h, v)]
@@ -81,7 +79,7 @@ __global__ __launch_bounds__(256) void k_bnd_list(const uint16_t *__restrict__ l
         const bool fin = u < INFINITY;
         const kd_h8 *lp = reinterpret_cast<const kd_h8 *>(lb + ((tile * nchunks) * 64 + lane) * 16);
         int cnt = 0;
-        uint16_t *mine = cand + row * KD_CAP + h * KD_HALF;
+        uint16_t *mine = cand + row * (2 * slot) + h * slot;
         // Two chunks per step (four 16-byte loads in flight per lane). Per chunk the smallest lb - S first (lb is
         // finite or -inf and S not NaN; a NaN difference, padding against padding, is never listed); only a chunk
         // with one at or below ub is looked at value by value.
@@ -103,7 +101,7 @@ __global__ __launch_bounds__(256) void k_bnd_list(const uint16_t *__restrict__ l
             while (mask) {
                 const int v = __ffs(mask) - 1;
                 mask &= mask - 1u;
-                if (cnt < KD_HALF) mine[cnt] = (uint16_t)km_bnd_centre(ch, h, v);
+                if (cnt < slot) mine[cnt] = (uint16_t)km_bnd_centre(ch, h, v);
                 cnt++;
             }
         };
@@ -125,7 +123,7 @@ __global__ __launch_bounds__(256) void k_bnd_list(const uint16_t *__restrict__ l
         const bool mine_row = real && h == 0;
         int code = KD_OVER;
         if (mine_row) {
-            if (fin && cnt <= KD_HALF && cnt_o <= KD_HALF && cnt + cnt_o > 0) code = cnt | (cnt_o << 8);
+            if (fin && cnt <= slot && cnt_o <= slot && cnt + cnt_o > 0) code = cnt | (cnt_o << 8);
             ub[row] = u;
             ncand[row] = (uint16_t)code;
         }
@@ -423,13 +421,13 @@ hipError_t km_launch_bnd_decide(km_bnd *bs, double max_visited, float *S, int k,
 }
 
 hipError_t km_launch_bnd_list(const uint16_t *lb, float *ub, const uint32_t *ubl, int64_t n, int k, int nchunks,
-                              const float *S, const float *delta, float hi, uint16_t *ncand, uint16_t *cand,
+                              const float *S, const float *delta, float hi, uint16_t *ncand, uint16_t *cand, int slot,
                               uint32_t *over, uint32_t *multi, km_control *ctl, km_bnd *bs, int cus, hipStream_t s) {
     const int64_t nwork = (n + 31) / 32;
     const int64_t blocks = std::min<int64_t>((nwork + 3) / 4, (int64_t)cus * 4);
     hipLaunchKernelGGL(k_bnd_list, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256),
                        (size_t)nchunks * 32 * sizeof(float), s, lb, ub, ubl, n, k, nchunks, S, delta, hi, ncand, cand,
-                       over, multi, ctl, &bs->skip_list);
+                       slot, over, multi, ctl, &bs->skip_list);
     return hipGetLastError();
 }
 

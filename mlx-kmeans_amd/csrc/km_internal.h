@@ -199,9 +199,9 @@ hipError_t km_launch_lowd(const km_lowd_plan &pl, const float *X, int64_t n, int
                           uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, const int32_t *stop,
                           hipStream_t s);
 
-// Wide rows (16 < dims <= KM_BIG_MAX_DIMS, k <= KM_BIG_MAX_K): bf16 MFMA screen keeping up to 16 keys per half-row,
-// exact rescoring of the
-// candidates, stable counting sort by label and per-cluster float64 sums.
+// Wide rows (16 < dims <= KM_BIG_MAX_DIMS, k <= KM_BIG_MAX_K): bf16 MFMA screen keeping up to 16 keys per half-row
+// (32 above 768 dims), exact rescoring of the candidates, stable counting sort by label and per-cluster float64
+// sums.
 struct km_big_plan {
     int ok;
     int DS;          // MFMA K-steps over the padded dims (16 DS >= dims)
@@ -219,6 +219,8 @@ struct km_big_plan {
 #define KM_BIG_MAX_DIMS 1536
 km_big_plan km_plan_big(int64_t n, int d, int k);
 size_t km_big_x16_elems(const km_big_plan &pl);   // uint16 elements of the bf16 row operands
+// candidate slots per half-row of the wide-row lists at d dims (16, 32 above 768 dims): cand holds 2 x this per row
+int km_big_list_slot(int d);
 size_t km_big_cop_elems(const km_big_plan &pl);   // uint16 elements of the bf16 centre operands
 hipError_t km_launch_big_rows(const km_big_plan &pl, const float *X, int64_t n, int d, uint16_t *X16T, float *xsq,
                               hipStream_t s);
@@ -343,7 +345,7 @@ hipError_t km_launch_bnd_resample(const float *sraw, const float *xsq, int64_t n
 // A pass on the bounds, one slice: candidate lists (ncand/cand/over/multi as the screen writes them) and every
 // row's raised ub; gated on bs->skip_list.
 hipError_t km_launch_bnd_list(const uint16_t *lb, float *ub, const uint32_t *ubl, int64_t n, int k, int nchunks,
-                              const float *S, const float *delta, float hi, uint16_t *ncand, uint16_t *cand,
+                              const float *S, const float *delta, float hi, uint16_t *ncand, uint16_t *cand, int slot,
                               uint32_t *over, uint32_t *multi, km_control *ctl, km_bnd *bs, int cus, hipStream_t s);
 // After the full scan of a slice's overflow rows: their ub from the exact best (when bs->built).
 hipError_t km_launch_bnd_overfix(const uint32_t *over, const km_control *ctl, const uint32_t *labels,
