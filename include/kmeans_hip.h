@@ -153,10 +153,10 @@ int64_t km_profile_passes(km_ctx *ctx, double *ms, int64_t cap);
 int32_t km_stream_probe(km_ctx *ctx, int64_t bytes, int32_t reps, double *gbps);
 
 /* Which path the last pass on ctx ran for its assignment (KM_PATH_ROWS, _MFMA or _FUSED), and the number of
- * rows in that pass the matrix-core screen could not settle alone: on the fused path (dims 16, 32, 64) rows with
+ * rows in that pass the matrix-core screen could not settle alone: on the fused path (16 to 64 dims) rows with
  * more than one centre inside the error window (or non-finite rows), scored against every centre; on the
- * wide-row path rows that took the full scan of every centre (more than 16 centres in a half-row's window, or
- * non-finite data). 0 on the other paths. */
+ * wide-row path rows that took the full scan of every centre (more than 16 centres in a half-row's window,
+ * 32 above 768 dims, or non-finite data). 0 on the other paths. */
 int32_t km_last_path(const km_ctx *ctx);
 int64_t km_last_fallback_rows(km_ctx *ctx);
 

@@ -70,6 +70,36 @@ def test_wide_rows_match_the_oracle(lib, n, d, k, parts):
     ctx.close()
 
 
+@pytest.mark.parametrize("d,ndup,overflow", [(1024, 40, False), (800, 40, False), (1536, 40, False),
+                                             (1024, 80, True), (768, 40, True), (768, 24, False)])
+def test_window_lists_at_their_capacity(lib, d, ndup, overflow):
+    """Rows N(0, 1) scored against ndup near-identical centres at the origin (indices 64 .. 64 + ndup - 1, spread
+    0.01 per dim) and 216 far ones (norm 100): every row's window holds all ndup near ones and no far one, ndup / 2
+    per half-row. A half-row lists up to 32 centres above 768 dims and 16 up to 768; past that the row takes the
+    full scan. Labels and best are the oracle's bit for bit either way (the rescoring's ascending order and strict
+    '<' over nearly equal distances), and the rows sent to the full scan are all rows or none."""
+    import oracle
+    rng = np.random.default_rng(d + ndup)
+    n, k = 4_000, 256
+    X = rng.standard_normal((n, d)).astype(np.float32)
+    far = rng.standard_normal((k, d))
+    C = (100.0 * far / np.linalg.norm(far, axis=1, keepdims=True)).astype(np.float32)
+    C[64:64 + ndup] = (0.01 * rng.standard_normal((ndup, d))).astype(np.float32)
+    ol, ob = oracle.assign(X, C)
+    ctx = lib.Context()
+    ctx.set_parts([X])
+    say(f"[gpu] window lists n={n} d={d} k={k} near centres={ndup}")
+    _, labels, best = ctx.run_pass(C, labels=True, best=True)
+    assert ctx.last_path() == "mfma"
+    fb = ctx.fallback_rows()
+    say(f"[gpu]   rows scored against every centre: {fb}")
+    assert np.all((ol >= 64) & (ol < 64 + ndup))
+    assert np.array_equal(labels, ol), np.flatnonzero(labels != ol)[:10]
+    assert np.array_equal(best.view(np.uint32), ob.view(np.uint32))
+    assert fb == (n if overflow else 0)
+    ctx.close()
+
+
 @pytest.mark.parametrize("d,k,parts", [(960, 48, 1), (1536, 24, 2)])
 def test_wide_rows_fit_loop_matches_single_steps(lib, d, k, parts):
     """km_fit's passes after the first add only the rows that changed cluster when at most half of them did, and
