@@ -350,6 +350,7 @@ static int add_part(km_ctx *c, const float *X, int64_t rows, int32_t where) {
     c->parts.push_back(p);
     c->n += rows;
     c->wd_ready = false;
+    c->open_frac = -1.0;   // the open-row rate was the previous data's
     return KM_OK;
 }
 
