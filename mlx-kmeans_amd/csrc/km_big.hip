@@ -607,7 +607,12 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen_b
 // single-candidate rows take their label in k_big_label1, and the sorted accumulation adds the distances.
 static constexpr int KB_RR = 64;      // rows per rescoring block
 static constexpr int KB_RT = 256;     // threads (= items per round) per rescoring block
-static constexpr int KB_RCH = 32;     // dims per LDS chunk
+static constexpr int KB_RCH = 32;     // dims per LDS chunk (the full scan's)
+// dims per LDS chunk of the rescoring (1M x 768 / 1536, k = 1024, us per rescoring: 16 dims 297 / 1078, three
+// blocks per CU but twice the barriers; 32 dims 248 / 808; 64 dims 454 / 1503, one block per CU)
+static constexpr int KB_SCH = 32;
+static constexpr int KB_SLN = KB_SCH / 4;        // lanes staging one row's (or item's) chunk as float4s
+static constexpr int KB_SRW = KB_RT / KB_SLN;    // rows (items) one staging step covers
 template <bool V4, bool LITE>
 __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__ X, int64_t n, int d,
                                                        const float *__restrict__ C, int k,
@@ -622,8 +627,8 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
     // row's result its upper bound (block-uniform)
     const bool refresh = bref.lb && bref.bs->built;
     __shared__ uint32_t rid[KB_RR];   // the block's rows: consecutive, or entries of the list
-    __shared__ float xs[KB_RR * (KB_RCH + 1)];
-    __shared__ float cs[KB_RT * (KB_RCH + 1)];
+    __shared__ float xs[KB_RR * (KB_SCH + 1)];
+    __shared__ float cs[KB_RT * (KB_SCH + 1)];
     __shared__ uint16_t it_c[KB_RR * 2 * KB_LIST_MAX];
     __shared__ uint8_t it_r[KB_RR * 2 * KB_LIST_MAX];
     __shared__ float it_s[KB_RR * 2 * KB_LIST_MAX];
@@ -668,10 +673,11 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
     }
     __syncthreads();
     const int items = first[KB_RR];
-    // staging: with V4 (dims a multiple of 4, rows 16-byte aligned) 8 consecutive lanes fetch one 32-float chunk
-    // as float4s - thread t takes float4 t % 8 of rows t / 8 + 32 u and of items t / 8 + 32 u; otherwise floats
-    constexpr int XPT = KB_RR * KB_RCH / KB_RT;   // x values staged per thread per chunk
-    constexpr int CPT = KB_RCH;                   // centre values staged per thread per chunk (KB_RT items)
+    // staging: with V4 (dims a multiple of 4, rows 16-byte aligned) KB_SLN consecutive lanes fetch one
+    // KB_SCH-float chunk as float4s - thread t takes float4 t % KB_SLN of rows and of items t / KB_SLN + KB_SRW u;
+    // otherwise floats
+    constexpr int XPT = KB_RR * KB_SCH / KB_RT;   // x values staged per thread per chunk
+    constexpr int CPT = KB_SCH;                   // centre values staged per thread per chunk (KB_RT items)
     for (int q0 = 0; q0 < items; q0 += KB_RT) {
         const int ni = (items - q0) < KB_RT ? (items - q0) : KB_RT;
         const int q = q0 + tid;
@@ -682,16 +688,16 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         if (V4) {
 #pragma unroll
             for (int u = 0; u < CPT / 4; u++) {
-                const int i = tid / 8 + 32 * u;
-                cbase[u] = i < ni ? C + (int64_t)it_c[q0 + i] * d + 4 * (tid % 8) : nullptr;
+                const int i = tid / KB_SLN + KB_SRW * u;
+                cbase[u] = i < ni ? C + (int64_t)it_c[q0 + i] * d + 4 * (tid % KB_SLN) : nullptr;
             }
         }
         auto fetch = [&](int j0) {
-            const int w = (d - j0) < KB_RCH ? (d - j0) : KB_RCH;
+            const int w = (d - j0) < KB_SCH ? (d - j0) : KB_SCH;
             if (V4) {
 #pragma unroll
                 for (int u = 0; u < XPT / 4; u++) {
-                    const int r = tid / 8 + 32 * u, p = tid % 8;
+                    const int r = tid / KB_SLN + KB_SRW * u, p = tid % KB_SLN;
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (r < nr && 4 * p < w) {   // each listed row once per pass: non-temporal
                         const kb_f4 q = __builtin_nontemporal_load(reinterpret_cast<const kb_f4 *>(X + (int64_t)rid[r] * d + j0 + 4 * p));
@@ -705,7 +711,7 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
 #pragma unroll
                 for (int u = 0; u < CPT / 4; u++) {
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (cbase[u] && 4 * (tid % 8) < w) v = *reinterpret_cast<const float4 *>(cbase[u] + j0);
+                    if (cbase[u] && 4 * (tid % KB_SLN) < w) v = *reinterpret_cast<const float4 *>(cbase[u] + j0);
                     cv[4 * u] = v.x;
                     cv[4 * u + 1] = v.y;
                     cv[4 * u + 2] = v.z;
@@ -715,50 +721,50 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
 #pragma unroll
                 for (int u = 0; u < XPT; u++) {
                     const int e = tid + KB_RT * u;
-                    const int r = e / KB_RCH, jj = e % KB_RCH;
+                    const int r = e / KB_SCH, jj = e % KB_SCH;
                     xv[u] = (r < nr && jj < w) ? X[(int64_t)rid[r] * d + j0 + jj] : 0.0f;
                 }
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
                     const int e = tid + KB_RT * u;
-                    const int i = e / KB_RCH, jj = e % KB_RCH;
+                    const int i = e / KB_SCH, jj = e % KB_SCH;
                     cv[u] = (i < ni && jj < w) ? C[(int64_t)it_c[q0 + i] * d + j0 + jj] : 0.0f;
                 }
             }
         };
         fetch(0);
-        for (int j0 = 0; j0 < d; j0 += KB_RCH) {
-            const int w = (d - j0) < KB_RCH ? (d - j0) : KB_RCH;
+        for (int j0 = 0; j0 < d; j0 += KB_SCH) {
+            const int w = (d - j0) < KB_SCH ? (d - j0) : KB_SCH;
             __syncthreads();
             if (V4) {
 #pragma unroll
                 for (int u = 0; u < XPT; u++)
-                    xs[(tid / 8 + 32 * (u / 4)) * (KB_RCH + 1) + 4 * (tid % 8) + (u % 4)] = xv[u];
+                    xs[(tid / KB_SLN + KB_SRW * (u / 4)) * (KB_SCH + 1) + 4 * (tid % KB_SLN) + (u % 4)] = xv[u];
 #pragma unroll
                 for (int u = 0; u < CPT; u++)
-                    cs[(tid / 8 + 32 * (u / 4)) * (KB_RCH + 1) + 4 * (tid % 8) + (u % 4)] = cv[u];
+                    cs[(tid / KB_SLN + KB_SRW * (u / 4)) * (KB_SCH + 1) + 4 * (tid % KB_SLN) + (u % 4)] = cv[u];
             } else {
 #pragma unroll
                 for (int u = 0; u < XPT; u++) {
                     const int e = tid + KB_RT * u;
-                    xs[(e / KB_RCH) * (KB_RCH + 1) + e % KB_RCH] = xv[u];
+                    xs[(e / KB_SCH) * (KB_SCH + 1) + e % KB_SCH] = xv[u];
                 }
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
                     const int e = tid + KB_RT * u;
-                    cs[(e / KB_RCH) * (KB_RCH + 1) + e % KB_RCH] = cv[u];
+                    cs[(e / KB_SCH) * (KB_SCH + 1) + e % KB_SCH] = cv[u];
                 }
             }
             __syncthreads();
-            if (j0 + KB_RCH < d) fetch(j0 + KB_RCH);
+            if (j0 + KB_SCH < d) fetch(j0 + KB_SCH);
             if (q < items) {
-                const float *xr = xs + ir * (KB_RCH + 1);
-                const float *cc = cs + tid * (KB_RCH + 1);
+                const float *xr = xs + ir * (KB_SCH + 1);
+                const float *cc = cs + tid * (KB_SCH + 1);
                 float sv = sacc;
                 // a whole chunk unrolled: its LDS reads issue ahead of the dependent sum (dims still ascending)
-                if (w == KB_RCH) {
+                if (w == KB_SCH) {
 #pragma unroll
-                    for (int jj = 0; jj < KB_RCH; jj++) {
+                    for (int jj = 0; jj < KB_SCH; jj++) {
                         const float t = xr[jj] - cc[jj];
                         sv = sv + t * t;
                     }
