@@ -596,23 +596,32 @@ __global__ __launch_bounds__(64 * KB_WAVES, DS > 48 ? 1 : 2) void k_big_screen_b
 
 // ------------------------------------------------------------------ exact rescoring
 
-// Block (256 threads) per 64 consecutive rows. Each (row, candidate) pair is a work item, items ordered by row and
-// then by ascending candidate index (each row's thread sorts its own list); a thread takes one item per round.
-// 32 dims at a time, the block stages its rows and its items' centres in LDS (coalesced loads, stride 33 floats
-// so lanes on different rows or items read different banks), the next chunk's loads in flight in registers while
-// the current chunk is used; every item carries its running direct-form sum across the chunks, so the dims are
-// added in ascending order. Then one thread per row takes its items in order with a strict '<': the rows loop
-// restricted to the candidates. Rows marked KB_OVER are left to k_big_fullscan. With LITE (passes that return no
-// per-row distances) the blocks take 64 entries at a time of the screen's list of rows with several candidates;
-// single-candidate rows take their label in k_big_label1, and the sorted accumulation adds the distances.
-static constexpr int KB_RR = 64;      // rows per rescoring block
-static constexpr int KB_RT = 256;     // threads (= items per round) per rescoring block
+// One wave (a block of 64 threads) per KB_RR consecutive rows. Each (row, candidate) pair is a work item, items
+// ordered by row and then by ascending candidate index (each row's lane sorts its own list); a lane takes one item
+// per round. KB_SCH dims at a time, the wave stages its rows and its items' centres in LDS (coalesced loads, stride
+// KB_SCH + 1 floats so lanes on different rows or items read different banks), the next chunk's loads in flight in
+// registers while the current chunk is used; every item carries its running direct-form sum across the chunks, so
+// the dims are added in ascending order. Then one lane per row takes its items in order with a strict '<': the
+// rows loop restricted to the candidates. The wave shares its LDS with no other wave, so ordering its own LDS
+// accesses takes no block barrier. Rows marked KB_OVER are left to k_big_fullscan. With LITE (passes that return
+// no per-row distances) the waves take KB_RR entries at a time of the screen's list of rows with several
+// candidates; single-candidate rows take their label in k_big_label1, and the sorted accumulation adds the
+// distances.
+static constexpr int KB_RR = 16;      // rows per rescoring wave
+static constexpr int KB_RT = 64;      // lanes (= items per round) per rescoring wave
 static constexpr int KB_RCH = 32;     // dims per LDS chunk (the full scan's)
-// dims per LDS chunk of the rescoring (1M x 768 / 1536, k = 1024, us per rescoring: 16 dims 297 / 1078, three
-// blocks per CU but twice the barriers; 32 dims 248 / 808; 64 dims 454 / 1503, one block per CU)
-static constexpr int KB_SCH = 32;
+static constexpr int KB_SCH = 32;     // dims per LDS chunk of the rescoring
 static constexpr int KB_SLN = KB_SCH / 4;        // lanes staging one row's (or item's) chunk as float4s
 static constexpr int KB_SRW = KB_RT / KB_SLN;    // rows (items) one staging step covers
+static constexpr int KB_RITEMS = KB_RR * 2 * KB_LIST_MAX;   // items of one wave's rows at most
+
+// orders this wave's LDS accesses: every lane's earlier reads and writes before any later one
+__device__ __forceinline__ void kb_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <bool V4, bool LITE>
 __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__ X, int64_t n, int d,
                                                        const float *__restrict__ C, int k,
@@ -624,63 +633,58 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
                                                        const int32_t *__restrict__ stop, km_bnd_refresh bref) {
     if (stop && *stop) return;
     // with per-centre bounds that describe every tile: each item's exact distance refreshes its bound, and each
-    // row's result its upper bound (block-uniform)
+    // row's result its upper bound (wave-uniform)
     const bool refresh = bref.lb && bref.bs->built;
-    __shared__ uint32_t rid[KB_RR];   // the block's rows: consecutive, or entries of the list
+    __shared__ uint32_t rid[KB_RR];   // the wave's rows: consecutive, or entries of the list
     __shared__ float xs[KB_RR * (KB_SCH + 1)];
     __shared__ float cs[KB_RT * (KB_SCH + 1)];
-    __shared__ uint16_t it_c[KB_RR * 2 * KB_LIST_MAX];
-    __shared__ uint8_t it_r[KB_RR * 2 * KB_LIST_MAX];
-    __shared__ float it_s[KB_RR * 2 * KB_LIST_MAX];
-    __shared__ int first[KB_RR + 1];
-    const int tid = threadIdx.x, lane = tid & 63;
+    __shared__ uint16_t it_c[KB_RITEMS];
+    __shared__ uint8_t it_r[KB_RITEMS];
+    __shared__ float it_s[KB_RITEMS];
+    const int lane = threadIdx.x;
     const int64_t total = LITE ? (int64_t)ctl->n_multi : n;
     for (int64_t r0 = (int64_t)blockIdx.x * KB_RR; r0 < total; r0 += (int64_t)gridDim.x * KB_RR) {
     const int nr = (int)((total - r0) < KB_RR ? (total - r0) : KB_RR);
-    __syncthreads();   // the previous chunk's LDS is no longer read
-    if (tid < nr) rid[tid] = LITE ? list[r0 + tid] : (uint32_t)(r0 + tid);
-    __syncthreads();
-    // item lists: thread r owns row r; an exclusive scan of the counts (wave 0) gives each row its slots
+    kb_wave_sync();   // the previous rows' LDS is no longer read
+    // item lists: lane r owns row r; an inclusive scan of the counts gives each row its slots
     int code = KB_OVER, cntr = 0;
-    if (tid < KB_RR && tid < nr) {
-        code = ncand[rid[tid]];
+    uint32_t myrow = 0;
+    if (lane < nr) {
+        myrow = LITE ? list[r0 + lane] : (uint32_t)(r0 + lane);
+        rid[lane] = myrow;
+        code = ncand[myrow];
         cntr = code == KB_OVER ? 0 : (code & 255) + (code >> 8);
     }
-    if (tid < 64) {
-        int incl = cntr;
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off);
-            if (lane >= off) incl += v;
-        }
-        first[tid] = incl - cntr;
-        if (tid == 63) first[KB_RR] = incl;
+    int incl = cntr;
+    for (int off = 1; off < KB_RR; off <<= 1) {
+        const int v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
     }
-    __syncthreads();
-    if (tid < nr && cntr > 0) {
-        const int b = first[tid];
+    const int items = __shfl(incl, KB_RR - 1);   // lanes past nr count nothing
+    const int b = incl - cntr;
+    if (lane < nr && cntr > 0) {
         int m = b;
         for (int half = 0; half < 2; half++) {
             const int nc = half ? code >> 8 : code & 255;
             for (int i = 0; i < nc; i++) {
-                const uint16_t v = cand[(int64_t)rid[tid] * (2 * slot) + half * slot + i];
+                const uint16_t v = cand[(int64_t)myrow * (2 * slot) + half * slot + i];
                 int j = m - 1;
                 while (j >= b && it_c[j] > v) { it_c[j + 1] = it_c[j]; j--; }
                 it_c[j + 1] = v;
-                it_r[m] = (uint8_t)tid;
+                it_r[m] = (uint8_t)lane;
                 m++;
             }
         }
     }
-    __syncthreads();
-    const int items = first[KB_RR];
+    kb_wave_sync();
     // staging: with V4 (dims a multiple of 4, rows 16-byte aligned) KB_SLN consecutive lanes fetch one
-    // KB_SCH-float chunk as float4s - thread t takes float4 t % KB_SLN of rows and of items t / KB_SLN + KB_SRW u;
+    // KB_SCH-float chunk as float4s - lane t takes float4 t % KB_SLN of rows and of items t / KB_SLN + KB_SRW u;
     // otherwise floats
-    constexpr int XPT = KB_RR * KB_SCH / KB_RT;   // x values staged per thread per chunk
-    constexpr int CPT = KB_SCH;                   // centre values staged per thread per chunk (KB_RT items)
+    constexpr int XPT = KB_RR * KB_SCH / KB_RT;   // x values staged per lane per chunk
+    constexpr int CPT = KB_SCH;                   // centre values staged per lane per chunk (KB_RT items)
     for (int q0 = 0; q0 < items; q0 += KB_RT) {
         const int ni = (items - q0) < KB_RT ? (items - q0) : KB_RT;
-        const int q = q0 + tid;
+        const int q = q0 + lane;
         const int ir = q < items ? (int)it_r[q] : 0;
         float sacc = 0.0f;
         float xv[XPT], cv[CPT];
@@ -688,8 +692,8 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         if (V4) {
 #pragma unroll
             for (int u = 0; u < CPT / 4; u++) {
-                const int i = tid / KB_SLN + KB_SRW * u;
-                cbase[u] = i < ni ? C + (int64_t)it_c[q0 + i] * d + 4 * (tid % KB_SLN) : nullptr;
+                const int i = lane / KB_SLN + KB_SRW * u;
+                cbase[u] = i < ni ? C + (int64_t)it_c[q0 + i] * d + 4 * (lane % KB_SLN) : nullptr;
             }
         }
         auto fetch = [&](int j0) {
@@ -697,11 +701,11 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
             if (V4) {
 #pragma unroll
                 for (int u = 0; u < XPT / 4; u++) {
-                    const int r = tid / KB_SLN + KB_SRW * u, p = tid % KB_SLN;
+                    const int r = lane / KB_SLN + KB_SRW * u, p = lane % KB_SLN;
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (r < nr && 4 * p < w) {   // each listed row once per pass: non-temporal
-                        const kb_f4 q = __builtin_nontemporal_load(reinterpret_cast<const kb_f4 *>(X + (int64_t)rid[r] * d + j0 + 4 * p));
-                        v = make_float4(q.x, q.y, q.z, q.w);
+                        const kb_f4 qv = __builtin_nontemporal_load(reinterpret_cast<const kb_f4 *>(X + (int64_t)rid[r] * d + j0 + 4 * p));
+                        v = make_float4(qv.x, qv.y, qv.z, qv.w);
                     }
                     xv[4 * u] = v.x;
                     xv[4 * u + 1] = v.y;
@@ -711,7 +715,7 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
 #pragma unroll
                 for (int u = 0; u < CPT / 4; u++) {
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (cbase[u] && 4 * (tid % KB_SLN) < w) v = *reinterpret_cast<const float4 *>(cbase[u] + j0);
+                    if (cbase[u] && 4 * (lane % KB_SLN) < w) v = *reinterpret_cast<const float4 *>(cbase[u] + j0);
                     cv[4 * u] = v.x;
                     cv[4 * u + 1] = v.y;
                     cv[4 * u + 2] = v.z;
@@ -720,13 +724,13 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
             } else {
 #pragma unroll
                 for (int u = 0; u < XPT; u++) {
-                    const int e = tid + KB_RT * u;
+                    const int e = lane + KB_RT * u;
                     const int r = e / KB_SCH, jj = e % KB_SCH;
                     xv[u] = (r < nr && jj < w) ? X[(int64_t)rid[r] * d + j0 + jj] : 0.0f;
                 }
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
-                    const int e = tid + KB_RT * u;
+                    const int e = lane + KB_RT * u;
                     const int i = e / KB_SCH, jj = e % KB_SCH;
                     cv[u] = (i < ni && jj < w) ? C[(int64_t)it_c[q0 + i] * d + j0 + jj] : 0.0f;
                 }
@@ -735,31 +739,31 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         fetch(0);
         for (int j0 = 0; j0 < d; j0 += KB_SCH) {
             const int w = (d - j0) < KB_SCH ? (d - j0) : KB_SCH;
-            __syncthreads();
+            kb_wave_sync();   // the previous chunk's LDS is no longer read
             if (V4) {
 #pragma unroll
                 for (int u = 0; u < XPT; u++)
-                    xs[(tid / KB_SLN + KB_SRW * (u / 4)) * (KB_SCH + 1) + 4 * (tid % KB_SLN) + (u % 4)] = xv[u];
+                    xs[(lane / KB_SLN + KB_SRW * (u / 4)) * (KB_SCH + 1) + 4 * (lane % KB_SLN) + (u % 4)] = xv[u];
 #pragma unroll
                 for (int u = 0; u < CPT; u++)
-                    cs[(tid / KB_SLN + KB_SRW * (u / 4)) * (KB_SCH + 1) + 4 * (tid % KB_SLN) + (u % 4)] = cv[u];
+                    cs[(lane / KB_SLN + KB_SRW * (u / 4)) * (KB_SCH + 1) + 4 * (lane % KB_SLN) + (u % 4)] = cv[u];
             } else {
 #pragma unroll
                 for (int u = 0; u < XPT; u++) {
-                    const int e = tid + KB_RT * u;
+                    const int e = lane + KB_RT * u;
                     xs[(e / KB_SCH) * (KB_SCH + 1) + e % KB_SCH] = xv[u];
                 }
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
-                    const int e = tid + KB_RT * u;
+                    const int e = lane + KB_RT * u;
                     cs[(e / KB_SCH) * (KB_SCH + 1) + e % KB_SCH] = cv[u];
                 }
             }
-            __syncthreads();
+            kb_wave_sync();
             if (j0 + KB_SCH < d) fetch(j0 + KB_SCH);
             if (q < items) {
                 const float *xr = xs + ir * (KB_SCH + 1);
-                const float *cc = cs + tid * (KB_SCH + 1);
+                const float *cc = cs + lane * (KB_SCH + 1);
                 float sv = sacc;
                 // a whole chunk unrolled: its LDS reads issue ahead of the dependent sum (dims still ascending)
                 if (w == KB_SCH) {
@@ -779,26 +783,26 @@ __global__ __launch_bounds__(KB_RT) void k_big_rescore(const float *__restrict__
         }
         if (q < items) it_s[q] = sacc;
     }
-    __syncthreads();
-    if (tid < nr && code != KB_OVER) {
+    kb_wave_sync();
+    if (lane < nr && code != KB_OVER) {
         float bst = INFINITY;
         uint32_t bl = 0;
-        for (int q = first[tid]; q < first[tid] + cntr; q++) {
+        for (int q = b; q < b + cntr; q++) {
             const float sq = it_s[q];
             if (sq < bst) { bst = sq; bl = (uint32_t)it_c[q]; }
         }
-        labels[rid[tid]] = bl;
-        best[rid[tid]] = bst;
+        labels[myrow] = bl;
+        best[myrow] = bst;
         if (refresh) {
             const float u = (bst >= 0.0f && bst < INFINITY) ? __builtin_sqrtf(bst) * bref.hi : INFINITY;
-            bref.ub[rid[tid]] = u < INFINITY ? u : INFINITY;
-            bref.ubl[rid[tid]] = bl;
+            bref.ub[myrow] = u < INFINITY ? u : INFINITY;
+            bref.ubl[myrow] = bl;
         }
     }
     if (refresh) {
         // lb_c = sqrt(s_c) lo + S_c (frame), rounded toward zero: s_c <= D_c (1 + g), so sqrt(s_c) lo is at most
         // sqrt(D_c) (1 - g); 1 - 2^-22 covers the float32 addition. A non-finite distance or drift writes 0.
-        for (int q = tid; q < items; q += KB_RT) {
+        for (int q = lane; q < items; q += KB_RT) {
             const int64_t r = rid[it_r[q]];
             const int c = it_c[q];
             const float sq = it_s[q], sc = bref.S[c];
@@ -1259,7 +1263,7 @@ hipError_t km_launch_big_rescore(const float *X, int64_t n, int d, const float *
                            labels, stop);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         const rescore_fn fn = v4 ? k_big_rescore<true, true> : k_big_rescore<false, true>;
-        hipLaunchKernelGGL(fn, dim3(chunks < 4096u ? chunks : 4096u), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
+        hipLaunchKernelGGL(fn, dim3(chunks < 16384u ? chunks : 16384u), dim3(KB_RT), 0, s, X, n, d, C, k, ncand, cand,
                            slot, multi, ctl, labels, best, stop, br);
     } else {
         const rescore_fn fn = v4 ? k_big_rescore<true, false> : k_big_rescore<false, false>;
