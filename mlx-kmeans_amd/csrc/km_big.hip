@@ -436,7 +436,7 @@ __device__ __forceinline__ void kb_screen_tile(
     for (int ch = 0; ch < nchunks; ch++) {
         f32x16 acc;
         screen_chunk(ch * SPC, acc);
-        float key[16];
+        float key[16], cmin = 0.0f;   // this chunk's smallest key
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
@@ -444,8 +444,9 @@ __device__ __forceinline__ void kb_screen_tile(
             // Without packing, key[v] is the matrix cores' result register itself: the first instruction to
             // read it must be compiled code, whose hazard tracking inserts the wait states an MFMA result needs
             // (inline assembly here read stale accumulators)
-            m1 = PACK ? kb_min(m1, key[v]) : fminf(m1, key[v]);
+            cmin = v == 0 ? key[0] : PACK ? kb_min(cmin, key[v]) : fminf(cmin, key[v]);
         }
+        m1 = PACK ? kb_min(m1, cmin) : fminf(m1, cmin);
         if (!BND && sample) {   // a sample tile: its raw values, 64 B per lane
             float4 *dst = reinterpret_cast<float4 *>(sdst + (int64_t)ch * 1024);
             dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -468,13 +469,11 @@ __device__ __forceinline__ void kb_screen_tile(
         if (approx) continue;
         const float mrow = kb_min(m1, kb_partner(m1, lane));
         const float Tp = key_bound(mrow);
-        uint64_t bal[16], any = 0;
+        // a key inside the window somewhere in the wave: this chunk's smallest one is (a NaN key is never inside)
+        if (__ballot(cmin <= Tp)) {
+            uint64_t bal[16];
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            bal[v] = __ballot(key[v] <= Tp);
-            any |= bal[v];
-        }
-        if (any) {
+            for (int v = 0; v < 16; v++) bal[v] = __ballot(key[v] <= Tp);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 if ((bal[v] >> lane) & 1ull) {
