@@ -420,11 +420,12 @@ __device__ __forceinline__ void kb_screen_tile(
     // this chunk's keys inside it appended to this lane's list in LDS (up to LH; a full list is first pruned
     // against the current bound, and if still full the row takes the full scan). Approximate mode keeps only the
     // smallest key.
-    float *list = reinterpret_cast<float *>(ring + 2 * SLK * 1024) + (size_t)wave * LH * 64 + lane;
+    // LH slots per lane and one more that takes the fast path's writes of keys outside the window
+    float *list = reinterpret_cast<float *>(ring + 2 * SLK * 1024) + (size_t)wave * (LH + 1) * 64 + lane;
     // without packed keys, the listed keys' centre indices (after the KB_WAVES lists of keys)
     uint16_t *lidx = reinterpret_cast<uint16_t *>(reinterpret_cast<float *>(ring + 2 * SLK * 1024) +
-                                                  (size_t)KB_WAVES * LH * 64) +
-                     (size_t)wave * LH * 64 + lane;
+                                                  (size_t)KB_WAVES * (LH + 1) * 64) +
+                     (size_t)wave * (LH + 1) * 64 + lane;
     // a sample tile of the per-centre bounds (32-bit arithmetic: a slice has fewer than 2^27 tiles)
     const bool sample = !BND && bnd.sraw && have && (uint32_t)tile % (uint32_t)bnd.sstride == 0u;
     float *sdst = sample ? bnd.sraw + ((int64_t)((uint32_t)tile / (uint32_t)bnd.sstride) * nchunks * 64 + lane) * 16
@@ -471,6 +472,20 @@ __device__ __forceinline__ void kb_screen_tile(
         const float Tp = key_bound(mrow);
         // a key inside the window somewhere in the wave: this chunk's smallest one is (a NaN key is never inside)
         if (__ballot(cmin <= Tp)) {
+            int nin = 0;   // this lane's keys inside the window
+#pragma unroll
+            for (int v = 0; v < 16; v++) nin += key[v] <= Tp ? 1 : 0;
+            if (!__ballot(!spill && cnt + nin > LH)) {
+                // no lane's list fills up with a key still to come: every key is written at the lane's next slot
+                // (the spare slot once the list is full) and counted only when it is inside the window
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int sl = cnt < LH ? cnt : LH;
+                    if (!PACK) lidx[sl * 64] = (uint16_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
+                    list[sl * 64] = key[v];
+                    cnt += (key[v] <= Tp && cnt < LH) ? 1 : 0;
+                }
+            } else {
             uint64_t bal[16];
 #pragma unroll
             for (int v = 0; v < 16; v++) bal[v] = __ballot(key[v] <= Tp);
@@ -494,6 +509,7 @@ __device__ __forceinline__ void kb_screen_tile(
                         list[(cnt++) * 64] = key[v];
                     }
                 }
+            }
             }
         }
     }
@@ -1234,7 +1250,7 @@ hipError_t km_launch_big_screen(const km_big_plan &pl, int mode, const uint16_t 
     // below 64 dims the reference's dispatch runs its exact kernels (core.py:2036-2042)
     const int approx = (mode == KM_APPROX && d >= KM_APPROX_MIN_DIMS) ? 1 : 0;
     const int ak = pl.DS + 1, spc = (ak + kb_slice(pl.DS) - 1) / kb_slice(pl.DS), slk = (ak + spc - 1) / spc;
-    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * kb_list_half(pl.DS) * 64 * (pack ? 4 : 6);
+    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * (kb_list_half(pl.DS) + 1) * 64 * (pack ? 4 : 6);
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
@@ -1293,7 +1309,7 @@ static hipError_t kb_launch_screen_bnd(const km_big_plan &pl, const uint16_t *X1
                                        uint16_t *lb, float *ub, uint32_t *ubl, km_bnd *bs, int cus, hipStream_t s) {
     const float rho = (float)(1.01 * (double)(1u << pl.ib) * 0x1p-23);
     const int ak = DS + 1, spc = (ak + kb_slice(DS) - 1) / kb_slice(DS), slk = (ak + spc - 1) / spc;
-    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * kb_list_half(DS) * 64 * 4;
+    const size_t lds = 2 * (size_t)slk * 1024 + KB_WAVES * (kb_list_half(DS) + 1) * 64 * 4;
     if (lds > 65536) {
         hipError_t e = hipFuncSetAttribute((const void *)k_big_screen_bnd<DS>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds);
