@@ -64,6 +64,12 @@ __device__ __forceinline__ float kb_min(float a, float b) {
     asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
+// v_min3_f32: two v_min_f32 in a row by definition (the same result for every input, NaN included)
+__device__ __forceinline__ float kb_min3(float a, float b, float c) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 // value of lane l ^ 32
 __device__ __forceinline__ float kb_partner(float v, int lane) {
     const auto r = __builtin_amdgcn_permlane32_swap(kb_u32(v), kb_u32(v), false, false);
@@ -444,8 +450,10 @@ __device__ __forceinline__ void kb_screen_tile(
             key[v] = PACK ? kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx) : acc[v];
             // Without packing, key[v] is the matrix cores' result register itself: the first instruction to
             // read it must be compiled code, whose hazard tracking inserts the wait states an MFMA result needs
-            // (inline assembly here read stale accumulators)
-            cmin = v == 0 ? key[0] : PACK ? kb_min(cmin, key[v]) : fminf(cmin, key[v]);
+            // (inline assembly here read stale accumulators); packed keys go through v_min3 in pairs
+            if (!PACK) cmin = v == 0 ? key[0] : fminf(cmin, key[v]);
+            else if (v == 1) cmin = kb_min(key[0], key[1]);
+            else if (v >= 3 && (v & 1)) cmin = kb_min3(cmin, key[v - 1], key[v]);
         }
         m1 = PACK ? kb_min(m1, cmin) : fminf(m1, cmin);
         if (!BND && sample) {   // a sample tile: its raw values, 64 B per lane
@@ -472,18 +480,20 @@ __device__ __forceinline__ void kb_screen_tile(
         const float Tp = key_bound(mrow);
         // a key inside the window somewhere in the wave: this chunk's smallest one is (a NaN key is never inside)
         if (__ballot(cmin <= Tp)) {
-            int nin = 0;   // this lane's keys inside the window
+            // a lane whose list overflowed takes no more keys (its row takes the full scan): its bound is -inf
+            const float Tl = spill ? -INFINITY : Tp;
+            int nin = 0;   // this lane's keys to be listed
 #pragma unroll
-            for (int v = 0; v < 16; v++) nin += key[v] <= Tp ? 1 : 0;
-            if (!__ballot(!spill && cnt + nin > LH)) {
+            for (int v = 0; v < 16; v++) nin += key[v] <= Tl ? 1 : 0;
+            if (!__ballot(cnt + nin > LH)) {
                 // no lane's list fills up with a key still to come: every key is written at the lane's next slot
-                // (the spare slot once the list is full) and counted only when it is inside the window
+                // (at most the spare slot past the list, where a full or overflowed list stands) and counted only
+                // when it is listed
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int sl = cnt < LH ? cnt : LH;
-                    if (!PACK) lidx[sl * 64] = (uint16_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
-                    list[sl * 64] = key[v];
-                    cnt += (key[v] <= Tp && cnt < LH) ? 1 : 0;
+                    if (!PACK) lidx[cnt * 64] = (uint16_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
+                    list[cnt * 64] = key[v];
+                    cnt += key[v] <= Tl ? 1 : 0;
                 }
             } else {
             uint64_t bal[16];
