@@ -332,6 +332,11 @@ __device__ __forceinline__ void kb_screen_tile(
 #pragma unroll
     for (int q = 0; q < 8; q++) Bone[q] = (__bf16)((h == 0 && q < 2) ? 1.0f : 0.0f);
     const uint32_t IMASK = PACK ? (1u << ib) - 1u : 0u;
+    // up to 48 K-steps (two waves per SIMD) ~IMASK is held in a vector register, so that packing a key is one
+    // v_and_or_b32 with the index in a scalar register (768 dims: 1.58 -> 1.54 ms per screen); a lone wave per SIMD
+    // does better with the compiler's v_and + v_or3 (1536 dims: 3.45 ms against 3.51)
+    uint32_t nmask = ~IMASK;
+    if constexpr (DS <= 48) asm("v_mov_b32 %0, %1" : "=v"(nmask) : "s"(~IMASK));
     if (!PACK) approx = 0;
 
     // A operand slices: chunk ch is SPC slices of SLK K-steps (the last possibly shorter), staged through a
@@ -446,8 +451,11 @@ __device__ __forceinline__ void kb_screen_tile(
         float key[16], cmin = 0.0f;   // this chunk's smallest key
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + 4 * h + (v & 3));
-            key[v] = PACK ? kb_f32((kb_u32(acc[v]) & ~IMASK) | cidx) : acc[v];
+            // the packed index leaves out the half-row's own bit (4 h: bit 2 of every centre index), so it is the
+            // same in every lane; the list a key sits in, or the winning half-row, puts it back
+            uint32_t cidx = (uint32_t)(32 * ch + 8 * (v >> 2) + (v & 3));
+            if constexpr (DS <= 48) asm("s_or_b32 %0, %1, %2" : "=s"(cidx) : "s"(32 * ch), "n"(8 * (v >> 2) + (v & 3)));
+            key[v] = PACK ? kb_f32((kb_u32(acc[v]) & nmask) | cidx) : acc[v];
             // Without packing, key[v] is the matrix cores' result register itself: the first instruction to
             // read it must be compiled code, whose hazard tracking inserts the wait states an MFMA result needs
             // (inline assembly here read stale accumulators); packed keys go through v_min3 in pairs
@@ -523,7 +531,12 @@ __device__ __forceinline__ void kb_screen_tile(
             }
         }
     }
-    m1 = kb_min(m1, kb_partner(m1, lane));   // both halves of the row
+    // both halves of the row: the smaller key, half-row 0's on a tie (its centre index is the lower); hbit is the
+    // winning half-row's bit 2 of the minimiser's centre index
+    const float m1o = kb_partner(m1, lane);
+    const bool other = m1o < m1 || (m1o == m1 && h == 1) || (m1 != m1 && m1o == m1o);
+    const uint32_t hbit = (uint32_t)(other ? h ^ 1 : h) << 2;
+    m1 = kb_min(m1, m1o);
     const bool finite = xsq_up < INFINITY && m1 < 3.0e38f;
     if (!approx && finite && real_row) {
         // the final bound: keep the listed centres inside it
@@ -532,7 +545,8 @@ __device__ __forceinline__ void kb_screen_tile(
         for (int q = 0; q < cnt; q++) {
             const float kq = list[q * 64];
             if (kq <= Tp && (!BND || bnd.lists))
-                cand[row * (2 * LH) + h * LH + (w++)] = PACK ? (uint16_t)(kb_u32(kq) & IMASK) : lidx[q * 64];
+                cand[row * (2 * LH) + h * LH + (w++)] = PACK ? (uint16_t)((kb_u32(kq) & IMASK) | (uint32_t)(4 * h))
+                                                            : lidx[q * 64];
         }
         cnt = w;
     }
@@ -550,14 +564,14 @@ __device__ __forceinline__ void kb_screen_tile(
             u = __builtin_sqrtf(dm_up) * bnd.hi;
         }
         bnd.ub[row] = u < INFINITY ? u : INFINITY;
-        bnd.ubl[row] = kb_u32(m1) & IMASK;
+        bnd.ubl[row] = (kb_u32(m1) & IMASK) | hbit;
         if (!bnd.lists) return;
     }
     int code;
     if (!finite) {
         code = KB_OVER;   // non-finite data: the rows loop decides
     } else if (approx) {
-        cand[row * (2 * LH)] = (uint16_t)(kb_u32(m1) & IMASK);
+        cand[row * (2 * LH)] = (uint16_t)((kb_u32(m1) & IMASK) | hbit);
         code = 1;
     } else if (spill || spill_o || cnt + cnt_o == 0) {
         code = KB_OVER;   // an empty window cannot happen for finite data (the minimiser is inside it)
