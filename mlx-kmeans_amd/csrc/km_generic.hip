@@ -244,7 +244,11 @@ int km_reduce_splits(int nrb, int64_t kw, int cus) {
     // one 1024-thread block per CU at a time: keep the grid (entries / 64 x splits) within one round of blocks
     const int64_t cols = (kw + 63) / 64;
     if (kw <= KM_FIN1_MAX && cols * cap > cus) cap = (int)std::max<int64_t>(1, cus / cols);
-    int s = nrb / 16;
+    // with the single-block finish, about 256 partials per split (16 loads per thread of each block's sixteen
+    // sub-ranges): 10M x 32, k = 64 (512 partials) 17.1 us per reduce-and-finish at 8 splits, 13.3 at 2, 14.7 at
+    // 1; 100k x 32 (391 partials) 17.1 at 8, 13.2 at 2; 10M x 8 (over 3000 partials of 80 entries) 13.3 at 8,
+    // 20.1 at 2
+    int s = kw <= KM_FIN1_MAX ? (nrb + 255) / 256 : nrb / 16;
     if (s > cap) s = cap;
     if (s < 1) s = 1;
     return s;
