@@ -92,6 +92,7 @@ struct km_ctx {
     std::vector<int64_t> lstate_off;
     DBuf<float> Cb[2];      // centre buffers (k, d): pass p reads Cb[p & 1], writes Cb[(p + 1) & 1]
     DBuf<float> psum, pcomp;
+    DBuf<uint32_t> pmask;   // change-only fused passes: per row-block, the clusters whose partials it wrote
     DBuf<double> tot;
     DBuf<double> tot2;      // (k, 2) [count, best] totals recomputed for km_pass on the fused path
     DBuf<double> red;       // range sums of the reduce (S, k * (d + 2))
@@ -447,7 +448,7 @@ static int ensure_pass_buffers(km_ctx *c, int k, size_t total_rb, bool need_rows
 // Partials -> totals in c->tot, and with KM_FIN_UPDATE the new centres into Cb[(pass + 1) & 1] and the pass
 // statistics into the control block. presummed > 0: c->red already holds that many range sums.
 static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags, const int32_t *stop,
-                       int presummed = 0, const int32_t *dsel = nullptr) {
+                       int presummed = 0, const int32_t *dsel = nullptr, const uint32_t *pmask = nullptr) {
     const int d = c->d;
     const int64_t kw = (int64_t)k * (d + 2);
     float *Cn = c->Cb[(pass + 1) & 1].p;
@@ -455,7 +456,7 @@ static int finish_pass(km_ctx *c, int k, int rb, int pass, double tol, int flags
         const int S = km_reduce_splits(rb, kw, c->dev.cus);
         HIPCHK(c, launch(c, KK_REDUCE, [&] {
             return km_launch_reduce_finish(c->psum.p, c->pcomp.p, rb, kw, S, c->red.p, k, d, c->tot.p, Cn, c->ctl, pass,
-                                           tol, flags, stop, c->stream);
+                                           tol, flags, stop, c->stream, pmask);
         }));
         return KM_OK;
     }
@@ -710,6 +711,12 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
         }
         int r = ensure_pass_buffers(c, k, total_rb, false);
         if (r) return r;
+        // a change-only pass writes only the rows of partials its changed rows touched, and says which
+        uint32_t *pm = nullptr;
+        if (lmode == KM_LSTATE_DELTA) {
+            HIPCHK(c, c->pmask.ensure(total_rb * KM_PMASK_WORDS));
+            pm = c->pmask.p;
+        }
         // where the last fit saw few open rows, its change-only passes take the kernel without candidate lists
         const int scan_only = lmode == KM_LSTATE_DELTA && c->open_frac >= 0.0 && c->open_frac <= KM_SCAN_ONLY_FRAC;
         int rb = 0;
@@ -721,12 +728,13 @@ static int run_pass(km_ctx *c, int k, int mode, int path, uint32_t *labels_d, fl
             uint8_t *ls = lmode != KM_LSTATE_NONE ? c->lstate.p + c->lstate_off[i] : nullptr;
             HIPCHK(c, launch(c, KK_FUSED_MFMA, [&] {
                 return km_launch_mfma(plans[i], want_best, p.X, p.rows, d, Cin, k, lab, bst, c->psum.p, c->pcomp.p,
-                                      rb, c->ctl, ls, ls, lmode, stop, c->stream, scan_only);
+                                      rb, c->ctl, ls, ls, lmode, stop, c->stream, scan_only, pm);
             }));
             rb += plans[i].nrb;
             row0 += p.rows;
         }
-        return finish_pass(c, k, rb, pass, tol, flags | (lmode == KM_LSTATE_DELTA ? KM_FIN_DELTA : 0), stop);
+        return finish_pass(c, k, rb, pass, tol, flags | (lmode == KM_LSTATE_DELTA ? KM_FIN_DELTA : 0), stop, 0,
+                           nullptr, pm);
     }
 
     if (fam == FAM_LOWD) {

@@ -256,9 +256,14 @@ int km_reduce_splits(int nrb, int64_t kw, int cus) {
 
 // Block (x, y) of 1024 threads: entries 64 x .. 64 x + 63, range y of the S ranges of row-blocks. COHERENT: the range
 // sums are written with device-scope stores (through to the point of coherence, no L2-wide write-back).
+// With pmask, a row-block's entries of the clusters its mask leaves clear are zeros it did not write (their memory
+// holds whatever an earlier pass left): each is read with the others, so the loads stay batched, and replaced by
+// +0.0, which leaves the sum as it was (it starts at +0.0 and never becomes -0.0) - the same bits as without the
+// mask.
 template <bool COHERENT>
 __device__ void reduce_split_body(const float *__restrict__ psum, const float *__restrict__ pcomp, int nrb, int64_t kw,
-                                  int S, double *__restrict__ tmp, double (*part)[64]) {
+                                  int S, double *__restrict__ tmp, double (*part)[64], const uint32_t *__restrict__ pmask,
+                                  int wd) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t e = (int64_t)blockIdx.x * 64 + lane;
     const int sp = blockIdx.y;
@@ -267,8 +272,19 @@ __device__ void reduce_split_body(const float *__restrict__ psum, const float *_
     const int q0 = r0 + (int)((int64_t)len * wave / 16), q1 = r0 + (int)((int64_t)len * (wave + 1) / 16);
     double acc = 0.0;
     if (e < kw) {
+        if (!pmask) {
 #pragma unroll 4
-        for (int r = q0; r < q1; r++) acc += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
+            for (int r = q0; r < q1; r++) acc += (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
+        } else {
+            const int c = (int)(e / wd);   // the entry's cluster (wd = d + 2 entries per cluster)
+            const int word = c >> 5;
+            const uint32_t bit = 1u << (c & 31);
+#pragma unroll 4
+            for (int r = q0; r < q1; r++) {
+                const double v = (double)psum[(int64_t)r * kw + e] + (double)pcomp[(int64_t)r * kw + e];
+                acc += (pmask[(int64_t)r * KM_PMASK_WORDS + word] & bit) ? v : 0.0;
+            }
+        }
     }
     part[wave][lane] = acc;
     __syncthreads();
@@ -282,16 +298,18 @@ __device__ void reduce_split_body(const float *__restrict__ psum, const float *_
 
 __global__ __launch_bounds__(1024) void k_reduce_split(const float *__restrict__ psum,
                                                        const float *__restrict__ pcomp, int nrb, int64_t kw, int S,
-                                                       double *__restrict__ tmp, const int32_t *__restrict__ stop) {
+                                                       double *__restrict__ tmp, const int32_t *__restrict__ stop,
+                                                       const uint32_t *__restrict__ pmask, int w) {
     if (stop && *stop) return;
     __shared__ double part[16][64];
-    reduce_split_body<false>(psum, pcomp, nrb, kw, S, tmp, part);
+    reduce_split_body<false>(psum, pcomp, nrb, kw, S, tmp, part, pmask, w);
 }
 
 hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
-                                  const int32_t *stop, hipStream_t s) {
+                                  const int32_t *stop, hipStream_t s, const uint32_t *pmask, int w) {
+    if (pmask && (w < 1 || kw % w != 0 || kw / w > 32 * KM_PMASK_WORDS)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_reduce_split, dim3((unsigned)((kw + 63) / 64), S), dim3(1024), 0, s, psum, pcomp, nrb, kw,
-                       S, tmp, stop);
+                       S, tmp, stop, pmask, w);
     return hipGetLastError();
 }
 
@@ -467,12 +485,13 @@ __global__ __launch_bounds__(1024) void k_reduce_finish(const float *__restrict_
                                                         double *__restrict__ tmp, int k, int d,
                                                         double *__restrict__ tot, float *__restrict__ Cnext,
                                                         km_control *__restrict__ ctl, int pass, double tol, int flags,
-                                                        const int32_t *__restrict__ stop) {
+                                                        const int32_t *__restrict__ stop,
+                                                        const uint32_t *__restrict__ pmask) {
     if (stop && *stop) return;
     __shared__ double part[16][64];
     __shared__ int s_last;
     extern __shared__ double Ts[];   // the totals, k * (d + 2) (used by the last block)
-    reduce_split_body<true>(psum, pcomp, nrb, kw, S, tmp, part);
+    reduce_split_body<true>(psum, pcomp, nrb, kw, S, tmp, part, pmask, d + 2);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's stores have completed
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -546,13 +565,14 @@ __global__ __launch_bounds__(256) void k_stats(const double *__restrict__ tot, i
 
 hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
                                    int k, int d, double *tot, float *Cnext, km_control *ctl, int pass, double tol,
-                                   int flags, const int32_t *stop, hipStream_t s) {
+                                   int flags, const int32_t *stop, hipStream_t s, const uint32_t *pmask) {
+    if (pmask && (kw != (int64_t)k * (d + 2) || k > 32 * KM_PMASK_WORDS)) return hipErrorInvalidValue;
     if (kw <= KM_FIN1_MAX && S <= KM_FIN1_SPLITS) {
         hipLaunchKernelGGL(k_reduce_finish, dim3((unsigned)((kw + 63) / 64), S), dim3(1024), (size_t)kw * sizeof(double),
-                           s, psum, pcomp, nrb, kw, S, tmp, k, d, tot, Cnext, ctl, pass, tol, flags, stop);
+                           s, psum, pcomp, nrb, kw, S, tmp, k, d, tot, Cnext, ctl, pass, tol, flags, stop, pmask);
         return hipGetLastError();
     }
-    hipError_t e = km_launch_reduce_split(psum, pcomp, nrb, kw, S, tmp, stop, s);
+    hipError_t e = km_launch_reduce_split(psum, pcomp, nrb, kw, S, tmp, stop, s, pmask, d + 2);
     if (e != hipSuccess) return e;
     return km_launch_finish(tmp, S, k, d, tot, Cnext, ctl, pass, tol, flags, stop, s);
 }

@@ -97,9 +97,13 @@ hipError_t km_launch_accum_generic(const km_accum_plan &pl, const float *X, int6
                                    float *pcomp, int rb0, const int32_t *stop, hipStream_t s);
 
 // Partials (nrb, k*w) sum+comp -> float64 sums of S = km_reduce_splits(nrb, k*w) fixed ranges: tmp (S, k*w).
+// pmask (optional, KM_PMASK_WORDS words per row-block): bit c set where the block wrote cluster c's row of
+// partials; a clear bit means that row is all zeros and was not written, and the reduce skips it (w = d + 2
+// entries per cluster row).
+#define KM_PMASK_WORDS 4
 int km_reduce_splits(int nrb, int64_t kw, int cus);
 hipError_t km_launch_reduce_split(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
-                                  const int32_t *stop, hipStream_t s);
+                                  const int32_t *stop, hipStream_t s, const uint32_t *pmask = nullptr, int w = 1);
 
 // Range sums -> totals (k, d+2). With KM_FIN_UPDATE also the new centres into Cnext and the pass statistics and
 // stopping rule into ctl (pass `pass`, tolerance tol); KM_FIN_SPHERICAL renormalises the new centres.
@@ -144,7 +148,7 @@ hipError_t km_launch_stream_read(const void *x, int64_t bytes, float *out, int b
 // finishes), else the two launches.
 hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nrb, int64_t kw, int S, double *tmp,
                                    int k, int d, double *tot, float *Cnext, km_control *ctl, int pass, double tol,
-                                   int flags, const int32_t *stop, hipStream_t s);
+                                   int flags, const int32_t *stop, hipStream_t s, const uint32_t *pmask = nullptr);
 
 // Greedy k-means++ on a device-resident sample of the rows, held transposed as ST (d x m) (km_seed.hip).
 // km_pp_trials(k) candidates per round (at most KM_PP_MAX_TRIALS); ws: km_pp_workspace(m, k) bytes; seeds_h:
@@ -179,11 +183,14 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
 #define KM_LSTATE_RECORD 1
 #define KM_LSTATE_DELTA 2
 // scan_only (KM_LSTATE_DELTA passes): the kernel without the candidate lists for waves with many open rows, every
-// open row scanned by the whole wave (smaller; for data whose open rows are rare).
+// open row scanned by the whole wave (smaller; for data whose open rows are rare). pmask (KM_LSTATE_DELTA passes,
+// optional): each block writes only the rows of partials of the clusters its changed rows left or joined (and
+// cluster 0's, which carries the inertia), and marks them in its KM_PMASK_WORDS words at pmask[(rb0 + block) *
+// KM_PMASK_WORDS]; the reduce must then be given the same pmask.
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
                           const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s,
-                          int scan_only = 0);
+                          int scan_only = 0, uint32_t *pmask = nullptr);
 
 // Fused single-read pass for dims <= 16: exact rows loop + deterministic accumulation into per-block partials.
 struct km_lowd_plan {

@@ -353,21 +353,23 @@ __global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_f
     const float *__restrict__ X, int64_t n, const float *__restrict__ C, int k,
     uint32_t *__restrict__ labels, float *__restrict__ best, float *__restrict__ psum, float *__restrict__ pcomp,
     int rb0, km_control *__restrict__ ctl, const uint8_t *__restrict__ lprev, uint8_t *__restrict__ lout,
-    const int32_t *__restrict__ stop) {
+    const int32_t *__restrict__ stop, uint32_t *__restrict__ pmask) {
     using G = Geo<D, KP>;
     using L = Lay<D>;
     constexpr int DH = G::DH, DS = G::DS, KT = G::KT, CS = G::CS, W = D + 2;
     constexpr int NT = (D + 31) / 32;                 // 32-dim tiles of the accumulation
     constexpr int FOLD = (KP * 32 * NT + 2 * KP) * 4; // bytes of the end-of-block fold per wave
-    // per wave: two block buffers, 64 uint16 labels and KP uint32 counts during the loop, the fold after it
+    // per wave: two block buffers, 64 uint16 labels, the clusters' change bits (TMB bytes) and KP uint32 counts
+    // during the loop, the fold after it (the change bits and counts stay in place)
     constexpr int LB = L::BUF + 64;                   // a block buffer: the rows, then their 64 previous labels
-    constexpr int LOOPB = 2 * LB + 256 + 4 * KP;     // + 64 uint16 labels (and 64 old labels)
+    constexpr int TMB = 16;                           // KM_PMASK_WORDS words
+    constexpr int LOOPB = 2 * LB + 256 + TMB + 4 * KP;   // + 64 uint16 labels (and 64 old labels)
     constexpr int LX = LM == 2 ? 1 : 0;               // loads per block beyond the rows' (the labels)
     // one-hot bytes in the block buffer once its rows are in registers: KP rows of OHS bytes (64 rows + 8 bytes
     // of padding, so the 32 lanes of a half-wave reading 8 bytes each start on distinct even banks)
     constexpr int OHS = 72, OHB_BYTES = KP * OHS;
     constexpr bool OHB = NT == 1 && OHB_BYTES <= L::BUF;
-    constexpr int WBYTES = (LOOPB > FOLD + 4 * KP) ? LOOPB : FOLD + 4 * KP;
+    constexpr int WBYTES = (LOOPB > FOLD + TMB + 4 * KP) ? LOOPB : FOLD + TMB + 4 * KP;
     constexpr int ABYTES = KT * DS * 64 * 16;         // the screen's centre operand, dims K-steps (per workgroup)
     // each float32 accumulator run covers at most FOLDB blocks (64 FOLDB rows) before it is added into sfold
     constexpr int FOLDB = 16;
@@ -395,6 +397,8 @@ __global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_f
     char *wbase = reinterpret_cast<char *>(lds + KP * CS) + ABYTES + wave * WBYTES;
     uint16_t *L16 = reinterpret_cast<uint16_t *>(wbase + 2 * LB);       // labels of the block (0x4000: no row)
     uint32_t *CNT = reinterpret_cast<uint32_t *>(wbase + WBYTES - 4 * KP);   // rows per centre (this wave)
+    uint32_t *TM = CNT - TMB / 4;   // LM 2: bit c set where a changed row of this wave left or joined cluster c
+    static_assert(TMB / 4 == KM_PMASK_WORDS && KP <= 32 * KM_PMASK_WORDS, "one bit per cluster");
 
     // blocks of 64 WAVES rows go round-robin to the workgroups (at any time the whole grid streams one window of
     // the rows), 64 rows per wave
@@ -473,6 +477,7 @@ __global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_f
         }
     int nblk = 0;
     for (int c = lane; c < KP; c += 64) CNT[c] = 0u;
+    if (LM == 2 && lane < TMB / 4) TM[lane] = 0u;
     const uint32_t ones = 0x00010001u, c3f80 = 0x3f803f80u, cneg = 0xc080c080u;
 
     // the two block buffers alternate by offset (pointer arithmetic keeps the LDS address space visible)
@@ -705,7 +710,11 @@ __global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_f
             if (LM != 2 || __ballot(moved)) {
             if (moved) {
                 atomicAdd(&CNT[bl], 1u);   // integer adds: the order does not matter
-                if (LM == 2) atomicAdd(&CNT[prv], 0xffffffffu);   // -1: the row left its old cluster
+                if (LM == 2) {
+                    atomicAdd(&CNT[prv], 0xffffffffu);   // -1: the row left its old cluster
+                    atomicOr(&TM[bl >> 5], 1u << (bl & 31));
+                    atomicOr(&TM[prv >> 5], 1u << (prv & 31));
+                }
             }
             if constexpr (OHB) {
                 // The block's rows in the accumulation's layout (lane = one dim, eight rows per K-step) go to
@@ -864,8 +873,23 @@ __global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_f
     float *ps = psum + (int64_t)(rb0 + blockIdx.x) * kw;
     float *pc = pcomp + (int64_t)(rb0 + blockIdx.x) * kw;
     const char *base = reinterpret_cast<const char *>(lds + KP * CS) + ABYTES;   // the first wave's region
+    // LM 2 with pmask: only the rows of clusters a changed row left or joined (and cluster 0's, which carries the
+    // inertia) are written, and the block's mask says which; every other row of its partials is zero
+    const bool masked = LM == 2 && pmask != nullptr;
+    __shared__ uint32_t bmask[TMB / 4];
+    if (masked) {
+        if (threadIdx.x < TMB / 4) {
+            uint32_t m = threadIdx.x == 0 ? 1u : 0u;
+            for (int w = 0; w < WAVES; w++)
+                m |= reinterpret_cast<const uint32_t *>(base + w * WBYTES + WBYTES - 4 * KP - TMB)[threadIdx.x];
+            bmask[threadIdx.x] = m;
+            pmask[(int64_t)(rb0 + blockIdx.x) * KM_PMASK_WORDS + threadIdx.x] = m;
+        }
+        __syncthreads();
+    }
     for (int e = threadIdx.x; e < k * W; e += 64 * WAVES) {
         const int c = e / W, col = e % W;
+        if (masked && !((bmask[c >> 5] >> (c & 31)) & 1u)) continue;
         float s = 0.0f, cc = 0.0f;
         if (col == 0) {
             uint32_t tot = 0;
@@ -899,7 +923,7 @@ __global__ __launch_bounds__(64 * WAVES, (D > 32 || KP >= 128) ? 1 : 2) void k_f
 // ------------------------------------------------------------------ planning and launch
 
 typedef void (*fused_fn)(const float *, int64_t, const float *, int, uint32_t *, float *, float *, float *,
-                         int, km_control *, const uint8_t *, uint8_t *, const int32_t *);
+                         int, km_control *, const uint8_t *, uint8_t *, const int32_t *, uint32_t *);
 
 // One entry per served shape: 4-wave blocks where the device gives a block enough LDS, 2-wave blocks otherwise.
 // Per block size: the pass without label state, with the rows' exact distances ("b": labels and best outputs),
@@ -933,8 +957,9 @@ static fused_entry g_fused[] = {
 // mirrors the kernel's layout: centres, the screen operand, then per wave max(two block buffers with their labels
 // + label staging + counts, fold + counts)
 static size_t lds_for(int d, int kp, int waves) {
-    const size_t loop = 2 * ((size_t)(64 * d * 4) + 64) + 256 + 4 * (size_t)kp;
-    const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float) + 4 * (size_t)kp;
+    const size_t tmb = 4 * KM_PMASK_WORDS;
+    const size_t loop = 2 * ((size_t)(64 * d * 4) + 64) + 256 + tmb + 4 * (size_t)kp;
+    const size_t fold = ((size_t)kp * 32 * ((d + 31) / 32) + 2 * (size_t)kp) * sizeof(float) + tmb + 4 * (size_t)kp;
     const size_t abytes = (size_t)(kp / 32) * ((d + 15) / 16) * 64 * 16;
     return (size_t)kp * ((d + 15) / 16 * 16 + 1) * sizeof(float) + abytes + waves * (loop > fold ? loop : fold);
 }
@@ -986,16 +1011,17 @@ km_mfma_plan km_plan_mfma(const km_device_info &dev, int64_t n, int d, int k, in
 hipError_t km_launch_mfma(const km_mfma_plan &pl, int want_best, const float *X, int64_t n, int d, const float *C,
                           int k, uint32_t *labels, float *best, float *psum, float *pcomp, int rb0, km_control *ctl,
                           const uint8_t *lprev, uint8_t *lout, int lmode, const int32_t *stop, hipStream_t s,
-                          int scan_only) {
+                          int scan_only, uint32_t *pmask) {
     const fused_entry *fe = find_fused(d, k);
     if (!fe || !pl.ok) return hipErrorInvalidValue;
     if (lmode != 0 && (want_best || !lout || (lmode == 2 && !lprev))) return hipErrorInvalidValue;
+    if (lmode != 2) pmask = nullptr;   // only the change-only passes leave rows of partials unwritten
     const bool w4 = pl.waves == 4;
     fused_fn fn = want_best ? (w4 ? fe->acc4b : fe->acc2b)
                   : lmode == 1 ? (w4 ? fe->acc4r : fe->acc2r)
                   : lmode == 2 ? (scan_only ? (w4 ? fe->acc4s : fe->acc2s) : (w4 ? fe->acc4i : fe->acc2i))
                                : (w4 ? fe->acc4 : fe->acc2);
     hipLaunchKernelGGL(fn, dim3(pl.nrb), dim3(64 * pl.waves), pl.lds, s, X, n, C, k, labels, best, psum,
-                       pcomp, rb0, ctl, lprev, lout, stop);
+                       pcomp, rb0, ctl, lprev, lout, stop, pmask);
     return hipGetLastError();
 }
