@@ -1089,23 +1089,31 @@ __global__ __launch_bounds__(1024) void k_big_scan(uint32_t *__restrict__ H, int
         counts[c] = run;
     }
     __syncthreads();
-    // exclusive prefix over labels: each thread a contiguous range, then the range totals
+    // exclusive prefix over labels: each thread a contiguous range, then the range totals in thread order by a
+    // scan within each wave and one over the sixteen wave totals (integer sums: any grouping gives the same)
     const int per = (k + 1023) / 1024;
     const int c0 = threadIdx.x * per, c1 = (c0 + per < k) ? c0 + per : k;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t s = 0;
     for (int c = c0; c < c1; c++) s += counts[c];
-    part[threadIdx.x] = s;
+    uint32_t incl = s;
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
+    }
+    if (lane == 63) part[wave] = incl;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (int t = 0; t < 1024; t++) {
-            const uint32_t v = part[t];
-            part[t] = run;
-            run += v;
+    if (wave == 0) {
+        const uint32_t t = lane < 16 ? part[lane] : 0u;
+        uint32_t ti = t;
+        for (int off = 1; off < 16; off <<= 1) {
+            const uint32_t y = __shfl_up(ti, off);
+            if (lane >= off) ti += y;
         }
+        if (lane < 16) part[16 + lane] = ti - t;   // the waves before this one
     }
     __syncthreads();
-    uint32_t run = part[threadIdx.x];
+    uint32_t run = part[16 + wave] + incl - s;
     for (int c = c0; c < c1; c++) {
         base[c] = run;
         run += counts[c];
