@@ -98,7 +98,8 @@ struct km_ctx {
     DBuf<double> red;       // range sums of the reduce (S, k * (d + 2))
     DBuf<uint32_t> labels;
     DBuf<float> best;
-    DBuf<float> pp_S, pp_C;     // k-means++: the row sample (transposed, dims x m) and the picked rows
+    DBuf<float> pp_S, pp_R, pp_C;   // k-means++: the row sample (transposed, dims x m; and rows, m x dims) and
+                                    // the picked rows
     DBuf<int64_t> pp_idx;       // k-means++: the sample's row indices, local to their slice
     DBuf<uint32_t> rl_st, rl_tie;   // relocation: selection state and per-block tie counts
     DBuf<int32_t> rl_empty;         // relocation: the empty clusters, ascending
@@ -282,6 +283,7 @@ extern "C" void km_destroy(km_ctx *c) {
     c->labels.release();
     c->best.release();
     c->pp_S.release();
+    c->pp_R.release();
     c->pp_C.release();
     c->pp_idx.release();
     c->pp_ws.release();
@@ -1146,6 +1148,7 @@ extern "C" int32_t km_seed_pp(km_ctx *c, int32_t k, const int64_t *sample, int64
     HIPCHK(c, hipSetDevice(c->device));
     const int d = c->d;
     HIPCHK(c, c->pp_S.ensure((size_t)m * d));
+    HIPCHK(c, c->pp_R.ensure((size_t)m * d));
     HIPCHK(c, c->pp_C.ensure((size_t)k * d));
     HIPCHK(c, c->pp_idx.ensure((size_t)m));
     HIPCHK(c, c->pp_ws.ensure(km_pp_workspace(m, k)));
@@ -1166,10 +1169,11 @@ extern "C" int32_t km_seed_pp(km_ctx *c, int32_t k, const int64_t *sample, int64
     HIPCHK(c, hipMemcpyAsync(c->pp_idx.p, local.data(), (size_t)m * sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
     HIPCHK(c, launch(c, KK_SEED_PP, [&] {
         for (size_t q = 0; q < c->parts.size(); q++) {
-            hipError_t e = km_launch_pp_gather(c->parts[q].X, c->pp_idx.p, j0s[q], j1s[q], m, d, c->pp_S.p, c->stream);
+            hipError_t e = km_launch_pp_gather(c->parts[q].X, c->pp_idx.p, j0s[q], j1s[q], m, d, c->pp_S.p, c->pp_R.p,
+                                               c->stream);
             if (e != hipSuccess) return e;
         }
-        return km_launch_pp(c->pp_S.p, m, d, k, first, seeds, c->pp_ws.p, c->pp_C.p, c->stream);
+        return km_launch_pp(c->pp_S.p, c->pp_R.p, m, d, k, first, seeds, c->pp_ws.p, c->pp_C.p, c->stream);
     }));
     HIPCHK(c, hipMemcpyAsync(C_out, c->pp_C.p, (size_t)k * d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));

@@ -150,16 +150,16 @@ hipError_t km_launch_reduce_finish(const float *psum, const float *pcomp, int nr
                                    int k, int d, double *tot, float *Cnext, km_control *ctl, int pass, double tol,
                                    int flags, const int32_t *stop, hipStream_t s, const uint32_t *pmask = nullptr);
 
-// Greedy k-means++ on a device-resident sample of the rows, held transposed as ST (d x m) (km_seed.hip).
-// km_pp_trials(k) candidates per round (at most KM_PP_MAX_TRIALS); ws: km_pp_workspace(m, k) bytes; seeds_h:
-// host, k - 1 round seeds; C: the k picked rows (device).
+// Greedy k-means++ on a device-resident sample of the rows, held transposed as ST (d x m) and row-major as SR
+// (m x d) (km_seed.hip). km_pp_trials(k) candidates per round (at most KM_PP_MAX_TRIALS); ws:
+// km_pp_workspace(m, k) bytes; seeds_h: host, k - 1 round seeds; C: the k picked rows (device).
 #define KM_PP_MAX_TRIALS 16
 int km_pp_trials(int k);
 size_t km_pp_workspace(int64_t m, int k);
 hipError_t km_launch_pp_gather(const float *X, const int64_t *idx, int64_t j0, int64_t j1, int64_t m, int d,
-                               float *ST, hipStream_t s);
-hipError_t km_launch_pp(const float *ST, int64_t m, int d, int k, int64_t first, const uint64_t *seeds_h, void *ws,
-                        float *C, hipStream_t s);
+                               float *ST, float *SR, hipStream_t s);
+hipError_t km_launch_pp(const float *ST, const float *SR, int64_t m, int d, int k, int64_t first,
+                        const uint64_t *seeds_h, void *ws, float *C, hipStream_t s);
 
 // MFMA-screened exact assignment. Fused variant also accumulates into partials (one per workgroup, which takes
 // blocks of 64 rows per wave round-robin).

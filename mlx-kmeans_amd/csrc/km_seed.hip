@@ -31,16 +31,19 @@ __device__ __forceinline__ uint64_t pp_mix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
-// ST[c][j] = X[idx[j]][c] for the sample rows j in [j0, j1) that fall in this slice (idx local to the slice):
-// the sample transposed, dims x m
+// ST[c][j] = SR[j][c] = X[idx[j]][c] for the sample rows j in [j0, j1) that fall in this slice (idx local to the
+// slice): the sample transposed, dims x m (a dim's rows contiguous, for the rows of an evaluation block), and as
+// rows, m x dims (a row's dims contiguous, for the round's candidates)
 __global__ __launch_bounds__(PP_THREADS) void k_pp_gather(const float *__restrict__ X, const int64_t *__restrict__ idx,
                                                           int64_t j0, int64_t j1, int64_t m, int d,
-                                                          float *__restrict__ ST) {
+                                                          float *__restrict__ ST, float *__restrict__ SR) {
     const int64_t total = (j1 - j0) * d;
     for (int64_t e = (int64_t)blockIdx.x * PP_THREADS + threadIdx.x; e < total; e += (int64_t)gridDim.x * PP_THREADS) {
         const int64_t j = j0 + e / d;
         const int c = (int)(e % d);
-        ST[(int64_t)c * m + j] = X[idx[j] * d + c];
+        const float v = X[idx[j] * d + c];
+        ST[(int64_t)c * m + j] = v;
+        SR[j * d + c] = v;
     }
 }
 
@@ -111,11 +114,13 @@ __global__ __launch_bounds__(PP_THREADS) void k_pp_pick(const float *__restrict_
 }
 
 // Per (row, trial): the minimum of d2 and the distance to the trial's candidate; per block and trial the float64
-// sum. A block takes PP_ROWS rows and PP_THREADS / PP_ROWS trials; the rows and the candidates pass through LDS
-// PP_DCHUNK dims at a time (each row read from HBM once per round), and each thread adds its pair's dims in
+// sum. A block takes PP_ROWS rows and PP_THREADS / PP_ROWS trials; the rows (from ST, a dim's 32 rows one
+// 128-byte line) and the candidates (from SR, a trial's chunk of dims contiguous: from ST each candidate value
+// would be a line of its own) pass through LDS PP_DCHUNK dims at a time, and each thread adds its pair's dims in
 // ascending order. Rows are padded by one float so that the 32 rows of a half-wave read distinct banks.
 static constexpr int PP_ROWS = 32, PP_DCHUNK = 256, PP_TPB = PP_THREADS / PP_ROWS;
-__global__ __launch_bounds__(PP_THREADS) void k_pp_eval(const float *__restrict__ ST, int64_t m, int d,
+__global__ __launch_bounds__(PP_THREADS) void k_pp_eval(const float *__restrict__ ST, const float *__restrict__ SR,
+                                                        int64_t m, int d,
                                                         const float *__restrict__ mins_prev, const uint32_t *__restrict__ best,
                                                         const double *__restrict__ ckey, const uint32_t *__restrict__ crow,
                                                         int nchunk, int trials, float *__restrict__ mins,
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(PP_THREADS) void k_pp_eval(const float *__restrict_
 #pragma unroll
         for (int q = 0; q < PP_TPB * PP_DCHUNK / PP_THREADS; q++) {
             const int e = tid + q * PP_THREADS, tt = e / PP_DCHUNK, c = e % PP_DCHUNK;
-            cv[q] = (c < w && blockIdx.y * PP_TPB + tt < trials) ? ST[(int64_t)(c0 + c) * m + sc[tt]] : 0.0f;
+            cv[q] = (c < w && blockIdx.y * PP_TPB + tt < trials) ? SR[(int64_t)sc[tt] * d + c0 + c] : 0.0f;
         }
 #pragma unroll
         for (int q = 0; q < PP_ROWS * PP_DCHUNK / PP_THREADS; q++) {
@@ -254,17 +259,17 @@ struct PpLayout {
 size_t km_pp_workspace(int64_t m, int k) { return PpLayout(m, k).bytes; }
 
 hipError_t km_launch_pp_gather(const float *X, const int64_t *idx, int64_t j0, int64_t j1, int64_t m, int d,
-                               float *ST, hipStream_t s) {
+                               float *ST, float *SR, hipStream_t s) {
     if (j1 <= j0) return hipSuccess;
     const int64_t total = (j1 - j0) * d;
     const int64_t blocks = (total + PP_THREADS - 1) / PP_THREADS;
     hipLaunchKernelGGL(k_pp_gather, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(PP_THREADS), 0, s, X, idx,
-                       j0, j1, m, d, ST);
+                       j0, j1, m, d, ST, SR);
     return hipGetLastError();
 }
 
-hipError_t km_launch_pp(const float *ST, int64_t m, int d, int k, int64_t first, const uint64_t *seeds_h, void *ws,
-                        float *C, hipStream_t s) {
+hipError_t km_launch_pp(const float *ST, const float *SR, int64_t m, int d, int k, int64_t first,
+                        const uint64_t *seeds_h, void *ws, float *C, hipStream_t s) {
     const int T = km_pp_trials(k);
     if (T > KM_PP_MAX_TRIALS) return hipErrorInvalidValue;
     const int nchunk = (int)((m + PP_CHUNK - 1) / PP_CHUNK), nblk = (int)((m + PP_ROWS - 1) / PP_ROWS);
@@ -285,7 +290,7 @@ hipError_t km_launch_pp(const float *ST, int64_t m, int d, int k, int64_t first,
         float *cur = mins[r & 1];
         hipLaunchKernelGGL(k_pp_pick, dim3(nchunk, T), dim3(PP_THREADS), 0, s, prev, best, m, T, seeds_h[r], ckey,
                            crow);
-        hipLaunchKernelGGL(k_pp_eval, dim3(nblk, (T + PP_TPB - 1) / PP_TPB), dim3(PP_THREADS), 0, s, ST, m, d, prev, best,
+        hipLaunchKernelGGL(k_pp_eval, dim3(nblk, (T + PP_TPB - 1) / PP_TPB), dim3(PP_THREADS), 0, s, ST, SR, m, d, prev, best,
                            ckey, crow, nchunk, T, cur, part, cand);
         hipLaunchKernelGGL(k_pp_commit, dim3(1), dim3(64 * T), 0, s, part, nblk, T, cand, best, picks, r);
         e = hipGetLastError();
