@@ -534,7 +534,8 @@ def test_fit_loop_totals_after_300_passes(lib, n, d, k, path):
 
 
 @pytest.mark.parametrize("d,k,parts,path", [(32, 64, 1, "mfma"), (16, 40, 2, "mfma"), (64, 32, 1, "mfma"),
-                                            (32, 20, 3, "mfma"), (16, 64, 1, "mfma"), (4, 12, 1, "fused"),
+                                            (32, 20, 3, "mfma"), (16, 64, 1, "mfma"), (32, 128, 2, "mfma"),
+                                            (24, 100, 1, "mfma"), (4, 12, 1, "fused"),
                                             (8, 8, 2, "fused"), (2, 40, 1, "fused"), (3, 30, 3, "fused"),
                                             (16, 8, 1, "fused"), (1, 200, 1, "fused"), (100, 100, 1, "wide"),
                                             (128, 300, 2, "wide"), (768, 64, 1, "wide"), (200, 40, 3, "wide")])
@@ -548,7 +549,8 @@ def test_fit_loop_change_accumulation_matches_full_steps(lib, d, k, parts, path)
     ("fused", with and without the screen) it accumulates every row each pass, and must agree all the same. On the
     wide-row path ("wide", reported as "mfma") a pass takes the change-only sums when at most n/2 rows changed, and
     the full accumulation otherwise; its inertia then comes from the totals in centred form. The data make both
-    happen within the passes."""
+    happen within the passes. A change-only pass of the matrix-core path writes only the partials of the clusters
+    its changed rows touched (a per-block mask of up to 128 clusters); 100 and 128 centres use every mask word."""
     rng = np.random.default_rng(900 + d + k + parts)
     n = 90_011
     cen = rng.uniform(-3, 3, size=(k, d)).astype(np.float32)
