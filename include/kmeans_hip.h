@@ -102,7 +102,8 @@ int32_t km_fit(km_ctx *ctx, const float *C0, int32_t k, int32_t max_iter, double
  * 2 + floor(ln k) candidates drawn with probability proportional to the squared distance to the nearest pick so
  * far (candidate t: the row with the largest d2 / (-ln u), u from splitmix64(seed_r ^ splitmix64(i * trials + t))),
  * the one that lowers the summed squared distance the most (first on a tie). C_out (host, k x dims): the picked
- * rows in pick order. Requires m >= k and 2 + floor(ln k) <= 16. */
+ * rows in pick order. Requires m >= k and 2 + floor(ln k) <= 16. The context keeps two device copies of the
+ * sample (dims x m and m x dims float32) and the rounds' minima (two trials x m float32 arrays). */
 int32_t km_seed_pp(km_ctx *ctx, int32_t k, const int64_t *sample, int64_t m, int64_t first, const uint64_t *seeds,
                    float *C_out);
 
