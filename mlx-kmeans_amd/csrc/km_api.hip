@@ -839,12 +839,14 @@ static int upload_centres(km_ctx *c, const float *C, int k) {
     return KM_OK;
 }
 
+// The host mirror is pinned: the copy reads it when the stream reaches it, and nothing writes the mirror before the
+// next read_control (a copy into it, ordered after this one) or a synchronisation, so the caller queues its passes
+// without waiting here.
 static int reset_control(km_ctx *c, double tol) {
-    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));   // no copy into the mirror is still in flight
     memset(c->ctl_h, 0, sizeof(km_control));
     c->ctl_h->tol = tol;
     HIPCHK(c, hipMemcpyAsync(c->ctl, c->ctl_h, sizeof(km_control), hipMemcpyHostToDevice, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
     return KM_OK;
 }
 
