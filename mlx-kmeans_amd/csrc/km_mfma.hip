@@ -955,7 +955,7 @@ static fused_entry g_fused[] = {
 #undef KM_FUSED
 
 // mirrors the kernel's layout: centres, the screen operand, then per wave max(two block buffers with their labels
-// + label staging + counts, fold + counts)
+// + label staging + change bits + counts, fold + change bits + counts)
 static size_t lds_for(int d, int kp, int waves) {
     const size_t tmb = 4 * KM_PMASK_WORDS;
     const size_t loop = 2 * ((size_t)(64 * d * 4) + 64) + 256 + tmb + 4 * (size_t)kp;
